@@ -1,0 +1,111 @@
+"""Seeded synthetic inputs for the five benchmark configurations of the W8A8 MoE-FFN path.
+
+    dq          DynamicQuant: fp16 x [1024, 4096] ~ N(0,1), 0.1% of entries x50 (outliers)
+    ardq        AddRmsNormDynamicQuant: bf16 x1, x2 [8192, 7168] ~ N(0,1), gamma ~ U(0.5, 1.5), eps 1e-6
+    qmm         QuantMatmul: int8 x1 [4096, 7168], x2 [7168, 4096] ~ U{-127..127},
+                scale ~ U(0.001, 0.01) [4096], pertoken ~ U(0.005, 0.02) [4096], bf16 out
+    gmsq_prefill  GroupedMatmulSwigluQuant: 131072 rows, K 7168, N 4096, E 256, group counts from a
+                multinomial over p_e ~ (e+1)^-1.1 (numpy default_rng(0)); x_scale ~ U(0.005, 0.02),
+                weight_scale ~ U(0.001, 0.01)
+    gmsq_decode GroupedMatmulSwigluQuant: 256 tokens x top-8 distinct experts chosen uniformly
+                (numpy default_rng(0), one draw per token) = 2048 rows; same shapes and scales,
+                followed by the int8 down-projection [2048, 2048] x [256, 2048, 7168] -> bf16.
+
+Group counts come from numpy (host, exact and portable).  Large tensors are drawn on the device with
+a seeded torch generator (one generator per tensor, seeds in listed order), so every run on the same
+software stack sees identical data; tests that need CPU copies of them copy slices back.
+`scale` < 1 shrinks the row/column counts for quick runs while keeping the group structure.
+"""
+import numpy as np
+import torch
+
+E_DEFAULT = 256
+
+
+def zipf_group_counts(rows, experts, a=1.1, seed=0):
+    p = (np.arange(experts) + 1.0) ** (-a)
+    p /= p.sum()
+    return np.random.default_rng(seed).multinomial(rows, p).astype(np.int64)
+
+
+def topk_group_counts(tokens, experts, k=8, seed=0):
+    rng = np.random.default_rng(seed)
+    ids = np.stack([rng.choice(experts, k, replace=False) for _ in range(tokens)])
+    return np.bincount(ids.ravel(), minlength=experts).astype(np.int64)
+
+
+def cumsum_list(counts):
+    return [int(v) for v in np.cumsum(counts)]
+
+
+def _gen(device, seed):
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def rand_i8(shape, device, seed):
+    return torch.randint(-127, 128, shape, dtype=torch.int8, device=device, generator=_gen(device, seed))
+
+
+def rand_uniform(shape, lo, hi, device, seed, dtype=torch.float32):
+    t = torch.rand(shape, dtype=torch.float32, device=device, generator=_gen(device, seed))
+    return (t * (hi - lo) + lo).to(dtype)
+
+
+def rand_normal(shape, device, seed, dtype=torch.float32):
+    return torch.randn(shape, dtype=torch.float32, device=device, generator=_gen(device, seed)).to(dtype)
+
+
+def make_dq(device="cuda", rows=1024, cols=4096, seed=0):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    n_out = max(1, int(round(0.001 * x.size)))
+    idx = rng.choice(x.size, n_out, replace=False)
+    x.reshape(-1)[idx] *= 50.0
+    return {"x": torch.from_numpy(x.astype(np.float16)).to(device)}
+
+
+def make_ardq(device="cuda", rows=8192, cols=7168, seed=0, dtype=torch.bfloat16):
+    return {
+        "x1": rand_normal((rows, cols), device, seed + 1, dtype),
+        "x2": rand_normal((rows, cols), device, seed + 2, dtype),
+        "gamma": rand_uniform((cols,), 0.5, 1.5, device, seed + 3, dtype),
+        "epsilon": 1e-6,
+    }
+
+
+def make_qmm(device="cuda", M=4096, K=7168, N=4096, seed=0):
+    return {
+        "x1": rand_i8((M, K), device, seed + 11),
+        "x2": rand_i8((K, N), device, seed + 12),
+        "scale": rand_uniform((N,), 0.001, 0.01, device, seed + 13),
+        "pertoken_scale": rand_uniform((M,), 0.005, 0.02, device, seed + 14),
+        "output_dtype": "bfloat16",
+    }
+
+
+def make_gmsq(device="cuda", counts=None, K=7168, N=4096, seed=0):
+    E = len(counts)
+    M = int(np.sum(counts))
+    return {
+        "x": rand_i8((M, K), device, seed + 21),
+        "weight": rand_i8((E, K, N), device, seed + 22),
+        "weight_scale": rand_uniform((E, N), 0.001, 0.01, device, seed + 23),
+        "x_scale": rand_uniform((M,), 0.005, 0.02, device, seed + 24),
+        "group_list": cumsum_list(counts),
+    }
+
+
+def make_gmsq_prefill(device="cuda", scale=1.0, seed=0):
+    rows = int(131072 * scale)
+    return make_gmsq(device, zipf_group_counts(rows, E_DEFAULT), seed=seed)
+
+
+def make_gmsq_decode(device="cuda", seed=0, with_down=True):
+    counts = topk_group_counts(256, E_DEFAULT)
+    d = make_gmsq(device, counts, seed=seed)
+    if with_down:
+        d["down_weight"] = rand_i8((E_DEFAULT, 2048, 7168), device, seed + 31)
+        d["down_weight_scale"] = rand_uniform((E_DEFAULT, 7168), 0.001, 0.01, device, seed + 32)
+    return d

@@ -1,0 +1,711 @@
+// gemm_i8.hpp - int8 x int8 -> int32 grouped GEMM cores for gfx950 with fused epilogues.
+//
+// All operators of the path share these cores:
+//   * GroupedMatmulSwigluQuant  (epilogue EPI_SWIGLU: per-token x per-channel dequant, SwiGLU with
+//     the gate in the left half, activation + per-row abs-max out; the int32 product never leaves
+//     the registers)
+//   * QuantMatmul and the int8 grouped down-projection (epilogue EPI_DEQUANT: the QuantMatmul
+//     dequant chain straight to bf16 / fp16)
+//
+// Weights are [E, K, N] with N contiguous (the reference layout, gmsq_launch.h:62-66).  The MFMA
+// B operand wants 16 consecutive K bytes per lane, so weight bytes are transposed in registers
+// with v_perm_b32 (4x4 byte blocks) on their way from HBM.
+//
+// Two cores:
+//   skinny_kernel  decode-shaped groups (<= 16 rows per pass).  One workgroup = (group, 256
+//                  weight columns); its 4 waves split K, stream the weight block straight from
+//                  HBM into MFMA operands (v_mfma_i32_16x16x64_i8, no LDS staging for B) and
+//                  reduce their int32 partials through LDS.  Weight bytes are read exactly once.
+//   tiled_kernel   prefill / dense shapes.  BM x 256 x 64 tiles staged through double-buffered
+//                  LDS, v_mfma_i32_32x32x32_i8, an XCD-aware grouped tile order, and row blocks
+//                  past a group's end skipped wave-uniformly.
+#pragma once
+
+#include "common.hpp"
+#include "host_util.hpp"
+
+namespace cb {
+
+enum { EPI_SWIGLU = 0, EPI_DEQUANT = 1, EPI_I32 = 2 };
+
+enum { BIAS_NONE = 0, BIAS_I32 = 1, BIAS_F16 = 2, BIAS_BF16 = 3, BIAS_F32 = 4 };
+
+// Epilogue parameters.
+//
+// EPI_DEQUANT computes, like the reference QuantMatmul epilogue
+// (quant_matmul_epilogue_kernel.cpp:15-22, 261-305):
+//   v = float(c); [v += bias (int32 kind)]; v *= scale[n]; [v += offset[n]];
+//   [v *= pertoken[row % pt_mod]]; [v += bias (float kinds)]; out = round16(v)
+// scale may be offset per group (scale_gstride elements) for the grouped down-projection.
+//
+// EPI_SWIGLU computes, like the reference GMSQ vector stage (gmsq_vec_kernel.cpp:15-20, 207-231):
+//   L = (float(c[j]) * xs[i]) * ws[g, j], R = (float(c[j+H]) * xs[i]) * ws[g, j+H]
+//   act = (L / (1 + exp(-L))) * R, stored fp32, and the running |act| max per row (atomic, as the
+//   bit pattern of a non-negative float).
+struct EpiArgs {
+    const void* scale;
+    int64_t scale_gstride;
+    int32_t scale_bf16;
+    int32_t scale_perchan;
+    const float* offset;
+    int32_t has_offset;
+    int32_t offset_perchan;
+    const float* pertoken;
+    int64_t pt_mod;
+    int32_t has_pt;
+    int32_t bias_kind;
+    const void* bias;
+    int32_t bias_perchan;
+    int32_t out_bf16;
+    int64_t bias_bstride;
+    void* out;  // fp16 / bf16 for EPI_DEQUANT, int32 for EPI_I32
+    int64_t out_bstride;
+    // SwiGLU
+    const float* w_scale;
+    const float* x_scale;
+    float* act;
+    u32* amax;
+    int64_t H;
+};
+
+struct GemmArgs {
+    const int8_t* x;
+    const int8_t* w;
+    int64_t M, K, N;
+    int64_t x_bstride, w_bstride;  // batch strides (dense QuantMatmul)
+    int64_t w_gstride;             // group stride of the weight (K * N)
+    int32_t ntiles;                // tiles along N
+    int32_t pad;
+    EpiArgs epi;
+    GroupTable gt;
+};
+
+__device__ __forceinline__ float load_scalar_any(const void* p, int kind, int64_t i)
+{
+    switch (kind) {
+        case BIAS_I32: return (float)((const int32_t*)p)[i];
+        case BIAS_F16: return f16_to_f32(((const uint16_t*)p)[i]);
+        case BIAS_BF16: return bf16_to_f32(((const uint16_t*)p)[i]);
+        default: return ((const float*)p)[i];
+    }
+}
+
+// Per-column part of the dequant chain, hoisted out of the row loop.
+struct ColDeq {
+    float scale, offset, bias;
+};
+
+__device__ __forceinline__ ColDeq col_deq(const EpiArgs& e, int64_t g, int64_t b, int64_t col)
+{
+    ColDeq d;
+    const int64_t si = e.scale_perchan ? col : 0;
+    d.scale = e.scale_bf16 ? bf16_to_f32(((const uint16_t*)e.scale)[g * e.scale_gstride + si])
+                           : ((const float*)e.scale)[g * e.scale_gstride + si];
+    d.offset = e.has_offset ? e.offset[e.offset_perchan ? col : 0] : 0.0f;
+    d.bias = e.bias_kind != BIAS_NONE
+                 ? load_scalar_any(e.bias, e.bias_kind, b * e.bias_bstride + (e.bias_perchan ? col : 0))
+                 : 0.0f;
+    return d;
+}
+
+__device__ __forceinline__ float apply_deq(const EpiArgs& e, const ColDeq& d, int c, float pt)
+{
+    float v = (float)c;
+    if (e.bias_kind == BIAS_I32) v = v + d.bias;
+    v = v * d.scale;
+    if (e.has_offset) v = v + d.offset;
+    if (e.has_pt) v = v * pt;
+    if (e.bias_kind >= BIAS_F16) v = v + d.bias;
+    return v;
+}
+
+__device__ __forceinline__ float swiglu(float gate_c, float up_c, float xs, float wsg, float wsu)
+{
+    const float L = (gate_c * xs) * wsg;
+    const float R = (up_c * xs) * wsu;
+    return (L / (1.0f + expf(-L))) * R;
+}
+
+__device__ __forceinline__ uint4 zero4() { return make_uint4(0u, 0u, 0u, 0u); }
+
+// Hide a value from loop-invariant code motion, so epilogue-only loads are not hoisted into
+// (and kept live across) the MFMA main loop.
+template <typename T>
+__device__ __forceinline__ T opaque(T v)
+{
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// Raw buffer resource over [base, base + bytes): loads at offsets >= bytes return zeros, which
+// zero-fills the K tail, and the per-lane address is one 32-bit VGPR instead of a 64-bit pointer.
+constexpr int kBufFlags = 0x00020000;  // dword3 of a raw (untyped, stride 0) gfx9 buffer descriptor
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufFlags);
+}
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff)
+{
+    const v4i v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
+    return make_uint4((u32)v[0], (u32)v[1], (u32)v[2], (u32)v[3]);
+}
+
+__device__ __forceinline__ uint2 buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t voff)
+{
+    typedef int v2i __attribute__((ext_vector_type(2)));
+    const v2i v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 0);
+    return make_uint2((u32)v[0], (u32)v[1]);
+}
+
+__device__ __forceinline__ v4i as_v4i(uint4 u)
+{
+    v4i r;
+    r[0] = (int)u.x;
+    r[1] = (int)u.y;
+    r[2] = (int)u.z;
+    r[3] = (int)u.w;
+    return r;
+}
+
+__device__ __forceinline__ u32 comp(const uint4& v, int i)
+{
+    return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+
+__device__ __forceinline__ void set_comp(uint4& v, int i, u32 x)
+{
+    if (i == 0) v.x = x;
+    else if (i == 1) v.y = x;
+    else if (i == 2) v.z = x;
+    else v.w = x;
+}
+
+// ============================================================================================
+// skinny_kernel: decode-shaped groups.
+//   grid = (ntiles, E), block = 256 (4 waves).  SwiGLU tiles cover 128 gate + 128 up columns,
+//   dequant tiles cover 256 columns.  Lane l of every wave owns k-group q = l / 16 and column
+//   group c = l % 16 (16 consecutive weight columns); after the in-register 16x16 byte transpose
+//   the lane holds 16 B operands, one per column, and MFMA j yields column (16 c + j).
+// ============================================================================================
+template <int EPI, bool PREFETCH>
+__global__ __launch_bounds__(256, PREFETCH ? 2 : 3) void skinny_kernel(const GemmArgs a)
+{
+    __shared__ int red[3][4][16][64];  // partial sums handed to the wave that owns them (48 KiB)
+
+    const int g = blockIdx.y;
+    const int r0 = g ? a.gt.row_end[g - 1] : 0;
+    const int r1 = a.gt.row_end[g];
+    if (r0 >= r1) return;
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int q = lane >> 4, c = lane & 15;
+    const int64_t K = a.K, N = a.N;
+    const EpiArgs& e = a.epi;
+
+    int64_t col;   // first weight column of this lane's group
+    int64_t ocol;  // first output column (act column for SwiGLU)
+    bool colok;
+    if constexpr (EPI == EPI_SWIGLU) {
+        const int64_t H = e.H;
+        ocol = (int64_t)blockIdx.x * 128 + 16 * (c & 7);
+        colok = ocol < H;
+        col = (c < 8) ? ocol : H + ocol;
+    } else {
+        ocol = (int64_t)blockIdx.x * 256 + 16 * c;
+        colok = ocol < N;
+        col = ocol;
+    }
+    const int64_t b = blockIdx.z;  // batch (dense QuantMatmul)
+    // weight block of this group; the host guarantees K * N < 2^31
+    const __amdgpu_buffer_rsrc_t wres = make_rsrc(a.w + b * a.w_bstride + (int64_t)g * a.w_gstride, (uint32_t)(K * N));
+    const uint32_t lane_off = (uint32_t)(colok ? col : 0) + (uint32_t)(q * 16) * (uint32_t)N;
+    const int nch = (int)((K + 63) >> 6);
+
+    for (int mb = r0; mb < r1; mb += 16) {
+        v4i acc[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[j] = v4i{0, 0, 0, 0};
+
+        const int arow = mb + c;
+        const bool arow_ok = arow < r1;
+        const int8_t* xr = a.x + b * a.x_bstride + (int64_t)(arow_ok ? arow : r0) * K;
+
+        auto load_chunk = [&](int kc, uint4 (&R)[16]) {
+            const uint32_t kofs = (uint32_t)(kc * 64) * (uint32_t)N;  // rows past K read as zeros
+#pragma unroll
+            for (int i = 0; i < 16; ++i) R[i] = buf_load16(wres, lane_off + kofs + (uint32_t)i * (uint32_t)N);
+        };
+        auto mma_chunk = [&](int kc, const uint4 (&R)[16]) {
+            const int64_t kb = (int64_t)kc * 64 + q * 16;
+            const uint4 A = (arow_ok && kb < K) ? *reinterpret_cast<const uint4*>(xr + kb) : zero4();
+            const v4i av = as_v4i(A);
+            // column block cb: the 4 B operands of columns 4 cb .. 4 cb + 3, built from dword cb
+            // of the 16 loaded rows, consumed right away to keep the live range short
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) {
+                uint4 T[4];
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) {
+                    u32 o0, o1, o2, o3;
+                    transpose4x4_b8(comp(R[4 * rb + 0], cb), comp(R[4 * rb + 1], cb),
+                                    comp(R[4 * rb + 2], cb), comp(R[4 * rb + 3], cb), o0, o1, o2, o3);
+                    set_comp(T[0], rb, o0);
+                    set_comp(T[1], rb, o1);
+                    set_comp(T[2], rb, o2);
+                    set_comp(T[3], rb, o3);
+                }
+#pragma unroll
+                for (int s4 = 0; s4 < 4; ++s4)
+                    acc[4 * cb + s4] =
+                        __builtin_amdgcn_mfma_i32_16x16x64_i8(av, as_v4i(T[s4]), acc[4 * cb + s4], 0, 0, 0);
+            }
+        };
+
+        if constexpr (PREFETCH) {
+            uint4 R[16];
+            if (wave < nch) load_chunk(wave, R);
+            for (int kc = wave; kc < nch; kc += 4) {
+                uint4 Rn[16];
+                if (kc + 4 < nch) load_chunk(kc + 4, Rn);
+                mma_chunk(kc, R);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) R[i] = Rn[i];
+            }
+        } else {
+            for (int kc = wave; kc < nch; kc += 4) {
+                uint4 R[16];
+                load_chunk(kc, R);
+                mma_chunk(kc, R);
+            }
+        }
+
+        // Cross-wave K reduction: wave w keeps accumulator row r == w and receives the other
+        // three waves' partials for it through LDS.
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (r != wave) {
+                const int slot = wave < r ? wave : wave - 1;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) red[slot][r][j][lane] = acc[j][r];
+            }
+        }
+        __syncthreads();
+        int s[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            int v = 0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (r == wave) v = acc[j][r];
+            s[j] = v + red[0][wave][j][lane] + red[1][wave][j][lane] + red[2][wave][j][lane];
+        }
+        __syncthreads();  // the next row block reuses red[]
+
+        // MFMA 16x16 C layout: lane l holds rows 4 (l / 16) + r, column l % 16.
+        const int row = mb + 4 * q + wave;
+        const bool rowok = row < r1;
+        if constexpr (EPI == EPI_SWIGLU) {
+            const int64_t H = e.H;
+            int u[16];  // the up-projection partner column sits 8 lanes away
+#pragma unroll
+            for (int j = 0; j < 16; ++j) u[j] = __shfl_xor(s[j], 8, 64);
+            float m = 0.0f;
+            if (c < 8 && rowok && colok) {
+                const float xs = e.x_scale[row];
+                const float* wsg = e.w_scale + (int64_t)g * N + opaque(ocol);
+                const float* wsu = wsg + H;
+                float act[16];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    act[j] = swiglu((float)s[j], (float)u[j], xs, wsg[j], wsu[j]);
+                    m = fmaxf(m, fabsf(act[j]));
+                }
+                float4* dst = reinterpret_cast<float4*>(e.act + (int64_t)row * H + ocol);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    dst[j] = make_float4(act[4 * j], act[4 * j + 1], act[4 * j + 2], act[4 * j + 3]);
+            }
+            m = fmaxf(m, __shfl_xor(m, 1, 64));
+            m = fmaxf(m, __shfl_xor(m, 2, 64));
+            m = fmaxf(m, __shfl_xor(m, 4, 64));
+            if (c == 0 && rowok) atomicMax(e.amax + row, __float_as_uint(m));
+        } else if constexpr (EPI == EPI_I32) {
+            if (rowok && colok) {
+                int4* dst = reinterpret_cast<int4*>((int32_t*)e.out + b * e.out_bstride + (int64_t)row * N + ocol);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) dst[j] = make_int4(s[4 * j], s[4 * j + 1], s[4 * j + 2], s[4 * j + 3]);
+            }
+        } else {
+            if (rowok && colok) {
+                const float pt = e.has_pt ? e.pertoken[row % e.pt_mod] : 1.0f;
+                const int64_t oc = opaque(ocol);
+                u32 packed[8];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const float v = apply_deq(e, col_deq(e, g, b, oc + j), s[j], pt);
+                    const u32 h = e.out_bf16 ? f32_to_bf16(v) : f32_to_f16(v);
+                    packed[j / 2] = (j & 1) ? (packed[j / 2] | (h << 16)) : h;
+                }
+                uint4* dst = reinterpret_cast<uint4*>((uint16_t*)e.out + b * e.out_bstride + (int64_t)row * N + ocol);
+                dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+                dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+            }
+        }
+    }
+}
+
+// ============================================================================================
+// tiled_kernel: prefill / dense.  BM x BN x 64 tiles, 4 waves in a WM x WN grid, 32x32x32 MFMA.
+// ============================================================================================
+constexpr int kNumXcd = 8;
+
+// Workgroups are dispatched round-robin over the 8 XCDs; renumber them so every XCD walks a
+// contiguous range of the tile order (tiles that share A rows / B columns share that XCD's L2).
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks)
+{
+    const int xcd = bid % kNumXcd, local = bid / kNumXcd;
+    const int per = (nblocks + kNumXcd - 1) / kNumXcd;
+    const int tall = nblocks % kNumXcd == 0 ? kNumXcd : nblocks % kNumXcd;
+    return xcd < tall ? xcd * per + local : tall * per + (xcd - tall) * (per - 1) + local;
+}
+
+__device__ __forceinline__ int group_of_tile(const GroupTable& gt, int mt)
+{
+    int lo = 0, hi = gt.n_groups - 1;
+    while (lo < hi) {  // last g with tile_start[g] <= mt and a non-empty tile range
+        const int mid = (lo + hi + 1) >> 1;
+        if (gt.tile_start[mid] <= mt) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+template <int EPI, int BM, int WM>
+struct TiledCfg {
+    static constexpr int BN = 256, BK = 64, PITCH = 80, WN = 4 / WM;
+    static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+    static constexpr int A_BYTES = BM * PITCH, B_BYTES = BN * PITCH;
+    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static constexpr int NA = BM / 64;  // 16-byte A chunks per thread per stage
+    static_assert(FM >= 1 && FN >= 2 && (FN % 2) == 0, "tile shape");
+};
+
+template <int EPI, int BM, int WM>
+__global__ __launch_bounds__(256, 1) void tiled_kernel(const GemmArgs a)
+{
+    using C = TiledCfg<EPI, BM, WM>;
+    constexpr int BN = C::BN, BK = C::BK, PITCH = C::PITCH, TM = C::TM, TN = C::TN, FM = C::FM,
+                  FN = C::FN, NA = C::NA, WN = C::WN;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::STAGE];
+
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int wm = wave / WN, wn = wave % WN;
+    const int64_t K = a.K, N = a.N;
+    const EpiArgs& e = a.epi;
+    const int64_t b = blockIdx.y;  // batch (dense QuantMatmul)
+
+    // ---- tile selection: XCD remap, then GROUP_M-swizzled (mt, nt) -------------------------
+    const int nblocks = gridDim.x;
+    const int pid = xcd_remap(blockIdx.x, nblocks);
+    constexpr int GROUP_M = 8;
+    const int T_m = a.gt.total_mtiles, T_n = a.ntiles;
+    const int per_group = GROUP_M * T_n;
+    const int gid = pid / per_group;
+    const int first_m = gid * GROUP_M;
+    const int gsz = (T_m - first_m) < GROUP_M ? (T_m - first_m) : GROUP_M;
+    const int mt = first_m + (pid % per_group) % gsz;
+    const int nt = (pid % per_group) / gsz;
+
+    const int g = group_of_tile(a.gt, mt);
+    const int rs = g ? a.gt.row_end[g - 1] : 0;
+    const int r1 = a.gt.row_end[g];
+    const int m0 = rs + (mt - a.gt.tile_start[g]) * BM;
+
+    const int8_t* xb = a.x + b * a.x_bstride;
+    const int8_t* wb = a.w + b * a.w_bstride + (int64_t)g * a.w_gstride;
+
+    // ---- global load assignment ------------------------------------------------------------
+    // A: chunk id = tid + 256 i -> tile row id / 4, k offset 16 (id % 4)
+    const int8_t* a_src[NA];
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+        const int id = tid + 256 * i;
+        int row = m0 + (id >> 2);
+        row = row < r1 ? row : r1 - 1;
+        a_src[i] = xb + (int64_t)row * K + (id & 3) * 16;
+    }
+    // B: thread -> 8 k rows (8 rg .. 8 rg + 7) x 8 tile columns (8 cg .. 8 cg + 7)
+    const int rg = tid & 7, cg = tid >> 3;
+    int64_t bcol;
+    bool bok;
+    if constexpr (EPI == EPI_SWIGLU) {
+        const int64_t H = e.H;
+        const int tc = 8 * cg;
+        const int64_t j = (int64_t)nt * (BN / 2) + (tc % (BN / 2));
+        bok = j < H;
+        bcol = tc < BN / 2 ? j : H + j;
+    } else {
+        bcol = (int64_t)nt * BN + 8 * cg;
+        bok = bcol < N;
+    }
+    const int8_t* b_src = wb + (bok ? bcol : 0) + (int64_t)(8 * rg) * N;
+
+    // wave-uniform skip of 32-row fragments that lie past the group end
+    bool fvalid[FM];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) fvalid[fm] = (m0 + wm * TM + fm * 32) < r1;
+
+    v16i acc[FM][FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0;
+
+    const int nk = (int)((K + BK - 1) / BK);
+    uint4 ra[NA];
+    uint2 rb[8];
+
+    auto gload = [&](int kt) {
+        const int64_t k0 = (int64_t)kt * BK;
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            const int id = tid + 256 * i;
+            ra[i] = (k0 + (id & 3) * 16 < K) ? *reinterpret_cast<const uint4*>(a_src[i] + k0) : zero4();
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            rb[i] = (k0 + 8 * rg + i < K) ? *reinterpret_cast<const uint2*>(b_src + (k0 + i) * N)
+                                          : make_uint2(0u, 0u);
+    };
+    auto lstore = [&](int buf) {
+        uint8_t* As = smem + buf * C::STAGE;
+        uint8_t* Bs = As + C::A_BYTES;
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+            const int id = tid + 256 * i;
+            *reinterpret_cast<uint4*>(As + (id >> 2) * PITCH + (id & 3) * 16) = ra[i];
+        }
+        // 8x8 byte transpose: rows 8 rg + i, columns 8 cg + s -> column-major k runs
+        u32 t[8][2];
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {      // row half (rows 4 hb .. 4 hb + 3)
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {  // column half
+                u32 o0, o1, o2, o3;
+                const u32 s0 = cb ? rb[4 * hb + 0].y : rb[4 * hb + 0].x;
+                const u32 s1 = cb ? rb[4 * hb + 1].y : rb[4 * hb + 1].x;
+                const u32 s2 = cb ? rb[4 * hb + 2].y : rb[4 * hb + 2].x;
+                const u32 s3 = cb ? rb[4 * hb + 3].y : rb[4 * hb + 3].x;
+                transpose4x4_b8(s0, s1, s2, s3, o0, o1, o2, o3);
+                t[4 * cb + 0][hb] = o0;
+                t[4 * cb + 1][hb] = o1;
+                t[4 * cb + 2][hb] = o2;
+                t[4 * cb + 3][hb] = o3;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            *reinterpret_cast<uint2*>(Bs + (8 * cg + s) * PITCH + 8 * rg) = make_uint2(t[s][0], t[s][1]);
+    };
+
+    auto tcol = [&](int fn) -> int {
+        if constexpr (EPI == EPI_SWIGLU)
+            return fn < FN / 2 ? wn * (TN / 2) + fn * 32 : BN / 2 + wn * (TN / 2) + (fn - FN / 2) * 32;
+        else
+            return wn * TN + fn * 32;
+    };
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) gload(kt + 1);
+        const uint8_t* As = smem + cur * C::STAGE;
+        const uint8_t* Bs = As + C::A_BYTES;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int ko = ks * 32 + (lane >> 5) * 16;
+            v4i af[FM], bf[FN];
+#pragma unroll
+            for (int fm = 0; fm < FM; ++fm)
+                af[fm] = *reinterpret_cast<const v4i*>(As + (wm * TM + fm * 32 + (lane & 31)) * PITCH + ko);
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn)
+                bf[fn] = *reinterpret_cast<const v4i*>(Bs + (tcol(fn) + (lane & 31)) * PITCH + ko);
+#pragma unroll
+            for (int fm = 0; fm < FM; ++fm) {
+                if (fvalid[fm]) {
+#pragma unroll
+                    for (int fn = 0; fn < FN; ++fn)
+                        acc[fm][fn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[fm], bf[fn], acc[fm][fn], 0, 0, 0);
+                }
+            }
+        }
+        if (kt + 1 < nk) lstore(cur ^ 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue.  32x32 C layout: lane l holds column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4
+    const int lr = (lane >> 5) * 4;
+    if constexpr (EPI == EPI_SWIGLU) {
+        const int64_t H = e.H;
+        float wsg[FN / 2], wsu[FN / 2];
+        int64_t jc[FN / 2];
+        bool jok[FN / 2];
+#pragma unroll
+        for (int fn = 0; fn < FN / 2; ++fn) {
+            jc[fn] = (int64_t)nt * (BN / 2) + wn * (TN / 2) + fn * 32 + (lane & 31);
+            jok[fn] = jc[fn] < H;
+            wsg[fn] = jok[fn] ? e.w_scale[(int64_t)g * N + jc[fn]] : 0.0f;
+            wsu[fn] = jok[fn] ? e.w_scale[(int64_t)g * N + H + jc[fn]] : 0.0f;
+        }
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) {
+            if (!fvalid[fm]) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm * TM + fm * 32 + (r >> 2) * 8 + lr + (r & 3);
+                const bool rowok = row < r1;
+                const float xs = rowok ? e.x_scale[row] : 0.0f;
+                float m = 0.0f;
+#pragma unroll
+                for (int fn = 0; fn < FN / 2; ++fn) {
+                    if (rowok && jok[fn]) {
+                        const float v = swiglu((float)acc[fm][fn][r], (float)acc[fm][fn + FN / 2][r], xs,
+                                               wsg[fn], wsu[fn]);
+                        e.act[(int64_t)row * H + jc[fn]] = v;
+                        m = fmaxf(m, fabsf(v));
+                    }
+                }
+#pragma unroll
+                for (int o = 1; o < 32; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+                if ((lane & 31) == 0 && rowok) atomicMax(e.amax + row, __float_as_uint(m));
+            }
+        }
+    } else if constexpr (EPI == EPI_I32) {
+        int32_t* ob = (int32_t*)e.out + b * e.out_bstride;
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) {
+            if (!fvalid[fm]) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm * TM + fm * 32 + (r >> 2) * 8 + lr + (r & 3);
+                if (row >= r1) continue;
+#pragma unroll
+                for (int fn = 0; fn < FN; ++fn) {
+                    const int64_t col = (int64_t)nt * BN + wn * TN + fn * 32 + (lane & 31);
+                    if (col < N) ob[(int64_t)row * N + col] = acc[fm][fn][r];
+                }
+            }
+        }
+    } else {
+        ColDeq cd[FN];
+        int64_t cc[FN];
+        bool cok[FN];
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+            cc[fn] = (int64_t)nt * BN + wn * TN + fn * 32 + (lane & 31);
+            cok[fn] = cc[fn] < N;
+            cd[fn] = col_deq(e, g, b, cok[fn] ? cc[fn] : 0);
+        }
+        uint16_t* ob = (uint16_t*)e.out + b * e.out_bstride;
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) {
+            if (!fvalid[fm]) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm * TM + fm * 32 + (r >> 2) * 8 + lr + (r & 3);
+                if (row >= r1) continue;
+                const float pt = e.has_pt ? e.pertoken[row % e.pt_mod] : 1.0f;
+#pragma unroll
+                for (int fn = 0; fn < FN; ++fn) {
+                    if (cok[fn]) {
+                        const float v = apply_deq(e, cd[fn], acc[fm][fn][r], pt);
+                        ob[(int64_t)row * N + cc[fn]] = e.out_bf16 ? f32_to_bf16(v) : f32_to_f16(v);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ============================================================================================
+// generic kernels: any K / N / alignment.  One thread per output, byte loads.  Used only for
+// shapes the vector paths do not cover (K % 16 != 0, N % 32 != 0, unaligned pointers).
+// ============================================================================================
+__device__ __forceinline__ int group_of_row(const GroupTable& gt, int row)
+{
+    int lo = 0, hi = gt.n_groups - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (gt.row_end[mid] > row) hi = mid;
+        else lo = mid + 1;
+    }
+    return lo;
+}
+
+__global__ __launch_bounds__(256) void generic_swiglu_kernel(const GemmArgs a)
+{
+    const int64_t H = a.epi.H;
+    const int row = (int)(blockIdx.x / a.ntiles);
+    const int64_t idx = (int64_t)(blockIdx.x % a.ntiles) * 256 + threadIdx.x;
+    const bool ok = idx < H;
+    const int g = group_of_row(a.gt, row);
+    float v = 0.0f;
+    if (ok) {
+        const int8_t* xr = a.x + (int64_t)row * a.K;
+        const int8_t* wg = a.w + (int64_t)g * a.w_gstride;
+        int cg = 0, cu = 0;
+        for (int64_t k = 0; k < a.K; ++k) {
+            const int xv = xr[k];
+            cg += xv * (int)wg[k * a.N + idx];
+            cu += xv * (int)wg[k * a.N + H + idx];
+        }
+        v = swiglu((float)cg, (float)cu, a.epi.x_scale[row], a.epi.w_scale[(int64_t)g * a.N + idx],
+                   a.epi.w_scale[(int64_t)g * a.N + H + idx]);
+        a.epi.act[(int64_t)row * H + idx] = v;
+    }
+    float m = wave_max(ok ? fabsf(v) : 0.0f);
+    if ((threadIdx.x & 63) == 0) atomicMax(a.epi.amax + row, __float_as_uint(m));
+}
+
+__global__ __launch_bounds__(256) void generic_dequant_kernel(const GemmArgs a)
+{
+    const int row = (int)(blockIdx.x / a.ntiles);
+    const int64_t col = (int64_t)(blockIdx.x % a.ntiles) * 256 + threadIdx.x;
+    const int64_t b = blockIdx.y;
+    if (col >= a.N) return;
+    const int g = group_of_row(a.gt, row);
+    const int8_t* xr = a.x + b * a.x_bstride + (int64_t)row * a.K;
+    const int8_t* wg = a.w + b * a.w_bstride + (int64_t)g * a.w_gstride;
+    int acc = 0;
+    for (int64_t k = 0; k < a.K; ++k) acc += (int)xr[k] * (int)wg[k * a.N + col];
+    const EpiArgs& e = a.epi;
+    const ColDeq d = col_deq(e, g, b, col);
+    const float pt = e.has_pt ? e.pertoken[row % e.pt_mod] : 1.0f;
+    const float v = apply_deq(e, d, acc, pt);
+    uint16_t* ob = (uint16_t*)e.out + b * e.out_bstride;
+    ob[(int64_t)row * a.N + col] = e.out_bf16 ? f32_to_bf16(v) : f32_to_f16(v);
+}
+
+__global__ __launch_bounds__(256) void generic_i32_kernel(const GemmArgs a)
+{
+    const int row = (int)(blockIdx.x / a.ntiles);
+    const int64_t col = (int64_t)(blockIdx.x % a.ntiles) * 256 + threadIdx.x;
+    const int64_t b = blockIdx.y;
+    if (col >= a.N) return;
+    const int g = group_of_row(a.gt, row);
+    const int8_t* xr = a.x + b * a.x_bstride + (int64_t)row * a.K;
+    const int8_t* wg = a.w + b * a.w_bstride + (int64_t)g * a.w_gstride;
+    int acc = 0;
+    for (int64_t k = 0; k < a.K; ++k) acc += (int)xr[k] * (int)wg[k * a.N + col];
+    ((int32_t*)a.epi.out + b * a.epi.out_bstride)[(int64_t)row * a.N + col] = acc;
+}
+
+}  // namespace cb

@@ -1,0 +1,320 @@
+// moe_ops.hip - C ABI entry points of the grouped / dense int8 GEMM operators:
+//   cb_grouped_matmul_swiglu_quant  (GroupedMatmulSwigluQuant)
+//   cb_grouped_matmul_quant         (int8 grouped down-projection)
+//   cb_quant_matmul                 (QuantMatmul)
+// plus the status strings.  Each entry point validates in the reference plugin's order, then
+// enqueues its kernels on the caller's stream without any allocation or host synchronisation.
+#include <cstring>
+
+#include "gemm_i8.hpp"
+
+namespace cb {
+
+// Phase 2 of GroupedMatmulSwigluQuant: per-token requant of the fp32 activation with the row
+// abs-max accumulated by the GEMM epilogue (gmsq_vec_kernel.cpp:233-257):
+//   amax <- FLT_MIN unless amax > FLT_MIN;  y_scale = amax * (1/127)
+//   y = rint16(clamp(act * (127 / amax), -128, 127))   (rint16 saturates)
+__global__ __launch_bounds__(256) void gmsq_requant_kernel(const float* __restrict__ act,
+                                                           const u32* __restrict__ amax, int64_t H,
+                                                           int8_t* __restrict__ y, float* __restrict__ ys)
+{
+    const int64_t row = blockIdx.x;
+    float a = __uint_as_float(amax[row]);
+    if (!(a > kFltMin)) a = kFltMin;
+    if (threadIdx.x == 0) ys[row] = a * kInv127;
+    const float inv = 127.0f / a;
+    const float* src = act + row * H;
+    int8_t* dst = y + row * H;
+    // clamp(v, -128, 127) then narrow == saturating rint16 for every non-NaN v; an all-zero row
+    // gives 0 * inf = NaN, which rint16 maps to 0
+    auto q = [&](float v) { return rint16(v * inv); };
+    if ((H & 3) == 0) {
+        for (int64_t j = (int64_t)threadIdx.x * 4; j < H; j += 1024) {
+            const float4 v = *reinterpret_cast<const float4*>(src + j);
+            *reinterpret_cast<u32*>(dst + j) = pack4_i8(q(v.x), q(v.y), q(v.z), q(v.w));
+        }
+    } else {
+        for (int64_t j = threadIdx.x; j < H; j += 256) dst[j] = (int8_t)q(src[j]);
+    }
+}
+
+__global__ void fill_u32_kernel(u32* p, int64_t n, u32 v)
+{
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+static void fill_u32(u32* p, int64_t n, u32 v, hipStream_t st)
+{
+    int64_t blocks = (n + 255) / 256;
+    blocks = blocks > 1024 ? 1024 : (blocks < 1 ? 1 : blocks);
+    hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p, n, v);
+}
+
+static inline int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+// Workspace layout of GroupedMatmulSwigluQuant: fp32 activation [M, H] then u32 row abs-max [M].
+struct GmsqWorkspace {
+    int64_t act_off, amax_off, total;
+};
+
+static GmsqWorkspace gmsq_workspace(int64_t M, int64_t N)
+{
+    GmsqWorkspace w;
+    const int64_t H = N / 2;
+    w.act_off = 0;
+    w.amax_off = round_up(M * H * 4, 256);
+    w.total = w.amax_off + round_up(M * 4, 256);
+    return w;
+}
+
+static constexpr int kSkinnyMaxRows = 32;  // groups up to this many rows take the skinny core
+static constexpr int kTiledBM = 128;
+#ifndef CB_SKINNY_PREFETCH
+#define CB_SKINNY_PREFETCH 1
+#endif
+static constexpr bool kSkinnyPrefetch = CB_SKINNY_PREFETCH;
+
+template <int EPI>
+static void launch_gemm(GemmArgs& a, const int64_t* gl, int64_t E, int64_t batch, bool fast, hipStream_t st)
+{
+    const int64_t Ncols = (EPI == EPI_SWIGLU) ? a.epi.H : a.N;  // output columns
+    build_group_table(a.gt, gl, E, kTiledBM);
+    if (!fast) {
+        a.ntiles = (int)((Ncols + 255) / 256);
+        const dim3 grid((unsigned)(a.M * a.ntiles), (unsigned)batch);
+        if constexpr (EPI == EPI_SWIGLU)
+            hipLaunchKernelGGL(generic_swiglu_kernel, grid, dim3(256), 0, st, a);
+        else if constexpr (EPI == EPI_I32)
+            hipLaunchKernelGGL(generic_i32_kernel, grid, dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL(generic_dequant_kernel, grid, dim3(256), 0, st, a);
+        return;
+    }
+    if (a.gt.max_rows <= kSkinnyMaxRows) {
+        a.ntiles = (int)((EPI == EPI_SWIGLU) ? (Ncols + 127) / 128 : (Ncols + 255) / 256);
+        const dim3 grid((unsigned)a.ntiles, (unsigned)E, (unsigned)batch);
+        hipLaunchKernelGGL((skinny_kernel<EPI, kSkinnyPrefetch>), grid, dim3(256), 0, st, a);
+        return;
+    }
+    a.ntiles = (int)((EPI == EPI_SWIGLU) ? (Ncols + 127) / 128 : (Ncols + 255) / 256);
+    const int64_t blocks = (int64_t)a.gt.total_mtiles * a.ntiles;
+    const dim3 grid((unsigned)blocks, (unsigned)batch);
+    hipLaunchKernelGGL((tiled_kernel<EPI, kTiledBM, 2>), grid, dim3(256), 0, st, a);
+}
+
+}  // namespace cb
+
+using namespace cb;
+
+extern "C" const char* cb_status_string(int s)
+{
+    switch (s) {
+        case CB_OK: return "ok";
+        case CB_ERR_NULL_POINTER: return "a required tensor pointer is NULL";
+        case CB_ERR_DTYPE: return "unsupported dtype";
+        case CB_ERR_SHAPE: return "invalid or unsupported shape";
+        case CB_ERR_K_MISMATCH: return "K mismatch between x and weight";
+        case CB_ERR_N_ODD: return "N must be even";
+        case CB_ERR_GROUP_LEN: return "group_list length must equal the expert count";
+        case CB_ERR_GROUP_COUNT: return "unsupported expert count";
+        case CB_ERR_GROUP_ORDER: return "group_list must be a cumsum <= M";
+        case CB_ERR_GROUP_TOTAL: return "group_list[-1] must equal M";
+        case CB_ERR_SCALE_LEN: return "scale / offset / pertoken / bias length mismatch";
+        case CB_ERR_ROW_TOO_LONG: return "row length must not exceed 16384";
+        case CB_ERR_WORKSPACE: return "workspace missing or too small";
+        case CB_ERR_EMPTY: return "non-empty shapes required";
+        case CB_ERR_LAUNCH: return "HIP kernel launch failed";
+        case CB_ERR_NO_DEVICE: return "no usable gfx950 device";
+        default: return "unknown status";
+    }
+}
+
+extern "C" const char* cb_version(void) { return "cannbench_amd 0.1 gfx950"; }
+
+extern "C" int64_t cb_grouped_matmul_swiglu_quant_workspace_size(int64_t M, int64_t K, int64_t N, int64_t E)
+{
+    (void)K;
+    (void)E;
+    if (M <= 0 || N <= 0) return 0;
+    return gmsq_workspace(M, N).total;
+}
+
+extern "C" int cb_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* weight, const float* weight_scale,
+                                              const float* x_scale, const int64_t* group_list,
+                                              int64_t group_len, int64_t M, int64_t K, int64_t N, int64_t E,
+                                              int8_t* y, float* y_scale, void* workspace,
+                                              int64_t workspace_bytes, void* stream)
+{
+    if (M < 0 || K < 0 || N < 0 || E < 0) return CB_ERR_SHAPE;
+    if (N % 2 != 0) return CB_ERR_N_ODD;  // GmsqMeta checks this before anything else
+    if (M == 0 || N == 0 || E == 0) return CB_OK;  // gmsq_plugin.cpp:93-95
+    if (!x || !weight || !weight_scale || !x_scale || !y || !y_scale) return CB_ERR_NULL_POINTER;
+    if (M > 0x7fffffffLL) return CB_ERR_SHAPE;
+    const int vs = validate_group_list(group_list, group_len, E, M);
+    if (vs != CB_OK) return vs;
+    const GmsqWorkspace ws = gmsq_workspace(M, N);
+    if (!workspace || workspace_bytes < ws.total) return CB_ERR_WORKSPACE;
+
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t H = N / 2;
+    uint8_t* wsb = (uint8_t*)workspace;
+    float* act = (float*)(wsb + ws.act_off);
+    u32* amax = (u32*)(wsb + ws.amax_off);
+
+    GemmArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.x = x;
+    a.w = weight;
+    a.M = M;
+    a.K = K;
+    a.N = N;
+    a.w_gstride = K * N;
+    a.epi.w_scale = weight_scale;
+    a.epi.x_scale = x_scale;
+    a.epi.act = act;
+    a.epi.amax = amax;
+    a.epi.H = H;
+
+    const bool fast = K > 0 && K % 16 == 0 && H % 16 == 0 && aligned(x, 16) && aligned(weight, 16) &&
+                      aligned(act, 16) && aligned(weight_scale, 4);
+    fill_u32(amax, M, 0u, st);
+    launch_gemm<EPI_SWIGLU>(a, group_list, E, 1, fast, st);
+    hipLaunchKernelGGL(gmsq_requant_kernel, dim3((unsigned)M), dim3(256), 0, st, act, amax, H, y, y_scale);
+    return check_launch();
+}
+
+extern "C" int cb_grouped_matmul_quant(const int8_t* x, const int8_t* weight, const float* weight_scale,
+                                       const float* x_scale, const int64_t* group_list, int64_t group_len,
+                                       int64_t M, int64_t K, int64_t N, int64_t E, void* out, void* stream)
+{
+    if (M < 0 || K < 0 || N < 0 || E < 0) return CB_ERR_SHAPE;
+    if (E < 1) return CB_ERR_GROUP_COUNT;  // grouped_matmul_plugin.cpp:133
+    if (M == 0 || N == 0) {
+        const int vs = validate_group_list(group_list, group_len, E, M);
+        return vs;
+    }
+    if (!x || !weight || !weight_scale || !x_scale || !out) return CB_ERR_NULL_POINTER;
+    if (M > 0x7fffffffLL) return CB_ERR_SHAPE;
+    const int vs = validate_group_list(group_list, group_len, E, M);
+    if (vs != CB_OK) return vs;
+
+    GemmArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.x = x;
+    a.w = weight;
+    a.M = M;
+    a.K = K;
+    a.N = N;
+    a.w_gstride = K * N;
+    a.epi.scale = weight_scale;
+    a.epi.scale_gstride = N;
+    a.epi.scale_perchan = 1;
+    a.epi.pertoken = x_scale;
+    a.epi.has_pt = 1;
+    a.epi.pt_mod = M;
+    a.epi.out = out;
+    a.epi.out_bf16 = 1;
+    const bool fast = K > 0 && K % 16 == 0 && N % 16 == 0 && aligned(x, 16) && aligned(weight, 16) &&
+                      aligned(out, 16);
+    launch_gemm<EPI_DEQUANT>(a, group_list, E, 1, fast, (hipStream_t)stream);
+    return check_launch();
+}
+
+extern "C" int cb_quant_matmul(const int8_t* x1, const int8_t* x2, const void* scale, int scale_dtype,
+                               int64_t scale_numel, const float* offset, int64_t offset_numel,
+                               const float* pertoken, int64_t pertoken_numel, const void* bias, int bias_dtype,
+                               int64_t bias_numel, int bias_batched, int64_t batch, int64_t M, int64_t K,
+                               int64_t N, int out_dtype, void* out, void* stream)
+{
+    // quant_matmul_plugin.cpp:86-175, in order.
+    if (!x1 || !x2 || !scale) return CB_ERR_NULL_POINTER;
+    if (scale_dtype != CB_DT_FLOAT32 && scale_dtype != CB_DT_BFLOAT16) return CB_ERR_DTYPE;
+    if (out_dtype != CB_DT_FLOAT16 && out_dtype != CB_DT_BFLOAT16) return CB_ERR_DTYPE;
+    if (K <= 0 || M <= 0 || N <= 0) return CB_ERR_EMPTY;
+    if (batch < 1 || M > 0x7fffffffLL) return CB_ERR_SHAPE;
+    if (scale_numel != 1 && scale_numel != N) return CB_ERR_SCALE_LEN;
+    if (offset_numel != 0) {
+        if (!offset) return CB_ERR_NULL_POINTER;
+        if (offset_numel != 1 && offset_numel != N) return CB_ERR_SCALE_LEN;
+    }
+    if (pertoken_numel != 0) {
+        if (!pertoken) return CB_ERR_NULL_POINTER;
+        if (pertoken_numel != M) return CB_ERR_SCALE_LEN;
+    }
+    int bias_kind = BIAS_NONE;
+    if (bias_numel != 0) {
+        if (!bias) return CB_ERR_NULL_POINTER;
+        switch (bias_dtype) {
+            case CB_DT_INT32: bias_kind = BIAS_I32; break;
+            case CB_DT_FLOAT16: bias_kind = BIAS_F16; break;
+            case CB_DT_BFLOAT16: bias_kind = BIAS_BF16; break;
+            case CB_DT_FLOAT32: bias_kind = BIAS_F32; break;
+            default: return CB_ERR_DTYPE;
+        }
+        if (bias_batched) {
+            if (!(batch > 1 && bias_numel == batch * N)) return CB_ERR_SCALE_LEN;
+        } else if (bias_numel != 1 && bias_numel != N) {
+            return CB_ERR_SCALE_LEN;
+        }
+    }
+    if (!out) return CB_ERR_NULL_POINTER;
+
+    GemmArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.x = x1;
+    a.w = x2;
+    a.M = M;
+    a.K = K;
+    a.N = N;
+    a.x_bstride = M * K;
+    a.w_bstride = K * N;
+    a.w_gstride = 0;
+    EpiArgs& e = a.epi;
+    e.scale = scale;
+    e.scale_bf16 = scale_dtype == CB_DT_BFLOAT16;
+    e.scale_perchan = scale_numel > 1;
+    e.offset = offset;
+    e.has_offset = offset_numel != 0;
+    e.offset_perchan = offset_numel > 1;
+    e.pertoken = pertoken;
+    e.has_pt = pertoken_numel != 0;
+    e.pt_mod = M;
+    e.bias = bias;
+    e.bias_kind = bias_kind;
+    e.bias_perchan = bias_batched ? (N > 1) : (bias_numel > 1);
+    e.bias_bstride = bias_batched ? N : 0;
+    e.out = out;
+    e.out_bf16 = out_dtype == CB_DT_BFLOAT16;
+    e.out_bstride = M * N;
+    const int64_t gl[1] = {M};
+    const bool fast = K % 16 == 0 && N % 16 == 0 && aligned(x1, 16) && aligned(x2, 16) && aligned(out, 16);
+    launch_gemm<EPI_DEQUANT>(a, gl, 1, batch, fast, (hipStream_t)stream);
+    return check_launch();
+}
+
+extern "C" int cb_grouped_matmul_int32(const int8_t* x, const int8_t* weight, const int64_t* group_list,
+                                       int64_t group_len, int64_t M, int64_t K, int64_t N, int64_t E,
+                                       int32_t* c, void* stream)
+{
+    if (M < 0 || K < 0 || N < 0 || E < 0) return CB_ERR_SHAPE;
+    if (E < 1) return CB_ERR_GROUP_COUNT;
+    const int vs = validate_group_list(group_list, group_len, E, M);
+    if (vs != CB_OK) return vs;
+    if (M == 0 || N == 0) return CB_OK;
+    if (!x || !weight || !c) return CB_ERR_NULL_POINTER;
+    if (M > 0x7fffffffLL) return CB_ERR_SHAPE;
+    GemmArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.x = x;
+    a.w = weight;
+    a.M = M;
+    a.K = K;
+    a.N = N;
+    a.w_gstride = K * N;
+    a.epi.out = c;
+    const bool fast = K > 0 && K % 16 == 0 && N % 16 == 0 && aligned(x, 16) && aligned(weight, 16) &&
+                      aligned(c, 16);
+    launch_gemm<EPI_I32>(a, group_list, E, 1, fast, (hipStream_t)stream);
+    return check_launch();
+}

@@ -1,0 +1,175 @@
+/*
+ * cannbench_amd.h - C ABI of the MI355X (gfx950) W8A8 MoE-FFN operator library.
+ *
+ * One C entry point per operator of the chain
+ *
+ *     AddRmsNormDynamicQuant -> GroupedMatmulSwigluQuant -> QuantMatmul / int8 GroupedMatmul
+ *     (+ DynamicQuant)
+ *
+ * Conventions shared by every entry point:
+ *   - Every tensor argument is a plain device pointer to a contiguous row-major buffer that the
+ *     caller owns.  The library never allocates device memory; operators that need scratch memory
+ *     take a `workspace` pointer sized by the matching *_workspace_size() query.
+ *   - `group_list` is a HOST array of int64 cumulative row counts (the reference passes it as an
+ *     `int[]` operator attribute): group g owns rows [group_list[g-1], group_list[g]), with
+ *     group_list[-1] taken as 0.  Empty groups are allowed; group_list[E-1] must equal M.
+ *   - Work is enqueued asynchronously on `stream` (a hipStream_t; NULL is the default stream).
+ *     Nothing synchronises and nothing is read back to the host.
+ *   - Every entry point validates its arguments first and returns a cb_status; on any error
+ *     nothing is launched.  cb_status_string() gives the message, worded like the reference's
+ *     TORCH_CHECK messages.
+ *   - Entry points are reentrant: the only global state is a per-device property cache.
+ */
+#ifndef CANNBENCH_AMD_H
+#define CANNBENCH_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  One per validation the reference performs with TORCH_CHECK. */
+typedef enum cb_status {
+    CB_OK = 0,
+    CB_ERR_NULL_POINTER = 1,       /* a required pointer is NULL                               */
+    CB_ERR_DTYPE = 2,              /* unsupported dtype code for this argument                 */
+    CB_ERR_SHAPE = 3,              /* a dimension is negative or shapes disagree              */
+    CB_ERR_K_MISMATCH = 4,         /* x.size(-1) != weight K                                  */
+    CB_ERR_N_ODD = 5,              /* GroupedMatmulSwigluQuant needs an even N                */
+    CB_ERR_GROUP_LEN = 6,          /* group_list length != expert count                       */
+    CB_ERR_GROUP_COUNT = 7,        /* expert count outside [1, CB_MAX_EXPERTS]                */
+    CB_ERR_GROUP_ORDER = 8,        /* group_list not a non-decreasing cumsum <= M             */
+    CB_ERR_GROUP_TOTAL = 9,        /* group_list[-1] != M                                     */
+    CB_ERR_SCALE_LEN = 10,         /* a scale / offset / bias has the wrong element count    */
+    CB_ERR_ROW_TOO_LONG = 11,      /* AddRmsNormDynamicQuant row length > 16384               */
+    CB_ERR_WORKSPACE = 12,         /* workspace missing or smaller than *_workspace_size()    */
+    CB_ERR_EMPTY = 13,             /* QuantMatmul requires non-empty M, K, N                 */
+    CB_ERR_LAUNCH = 14,            /* the HIP runtime refused a launch                       */
+    CB_ERR_NO_DEVICE = 15          /* no usable gfx950 device                                */
+} cb_status;
+
+/* dtype codes for the typed arguments. */
+typedef enum cb_dtype {
+    CB_DT_FLOAT16 = 1,
+    CB_DT_BFLOAT16 = 2,
+    CB_DT_FLOAT32 = 3,
+    CB_DT_INT8 = 4,
+    CB_DT_INT32 = 5
+} cb_dtype;
+
+/* Largest expert count accepted by the grouped operators (the reference accepts 64:
+ * operators/groupedmatmulswigluquant/csrc/ops/grouped_matmul_swiglu_quant/op_kernel/gmsq_launch.h:35). */
+#define CB_MAX_EXPERTS 256
+
+/* Largest AddRmsNormDynamicQuant row length (the reference's limit,
+ * operators/addrmsnormdynamicquant/csrc/ops/add_rms_norm_dynamic_quant/op_plugin/add_rms_norm_dynamic_quant_plugin.cpp:82-83). */
+#define CB_ARDQ_MAX_ROW 16384
+
+const char* cb_status_string(int status);
+
+/* Library version string, e.g. "cannbench_amd 0.1 gfx950". */
+const char* cb_version(void);
+
+/*
+ * AddRmsNormDynamicQuant.
+ * Replaces add_rms_norm_dynamic_quant(Tensor x1, Tensor x2, Tensor gamma, float epsilon)
+ *   -> (Tensor y, Tensor xOut, Tensor scaleOut)
+ * (operators/addrmsnormdynamicquant/csrc/ops/add_rms_norm_dynamic_quant/op_plugin/add_rms_norm_dynamic_quant_plugin.cpp:32,58-115)
+ * and its launchers launch_ardq_half / launch_ardq_bf16 (add_rms_norm_dynamic_quant_launch.h:33-40).
+ *
+ *   x1, x2   : dtype [rows, row_len]        (dtype = CB_DT_FLOAT16 or CB_DT_BFLOAT16)
+ *   gamma    : dtype [row_len]
+ *   y        : int8  [rows, row_len]
+ *   x_out    : dtype [rows, row_len]        x1 + x2 rounded to dtype
+ *   scale_out: fp32  [rows]
+ * rows == 0 or row_len == 0 returns CB_OK without a launch (the reference returns early).
+ */
+int cb_add_rms_norm_dynamic_quant(const void* x1, const void* x2, const void* gamma, int dtype,
+                                  int64_t rows, int64_t row_len, float epsilon, int8_t* y,
+                                  void* x_out, float* scale_out, void* stream);
+
+/*
+ * DynamicQuant (per-token symmetric int8).
+ * Replaces dynamic_quant(Tensor x) -> (Tensor y, Tensor scale)
+ * (operators/dynamicquant/csrc/ops/dynamic_quant/op_plugin/dynamic_quant_plugin.cpp:30,49-87).
+ *   x: dtype [rows, row_len] (fp16 / bf16), y: int8 [rows, row_len], scale: fp32 [rows].
+ */
+int cb_dynamic_quant(const void* x, int dtype, int64_t rows, int64_t row_len, int8_t* y,
+                     float* scale, void* stream);
+
+/*
+ * GroupedMatmulSwigluQuant.
+ * Replaces grouped_matmul_swiglu_quant(Tensor x, Tensor weight, Tensor weight_scale,
+ *   Tensor x_scale, int[] group_list) -> (Tensor y, Tensor y_scale)
+ * (operators/groupedmatmulswigluquant/csrc/ops/grouped_matmul_swiglu_quant/op_plugin/gmsq_plugin.cpp:40-41,67-145)
+ * and the launcher pair launch_gmsq_cube + launch_gmsq_vec (op_kernel/gmsq_launch.h:67-80).
+ *
+ *   x            int8 [M, K]        weight       int8 [E, K, N]  (N contiguous)
+ *   weight_scale fp32 [E, N]        x_scale      fp32 [M]
+ *   group_list   host int64 [group_len] cumulative counts
+ *   y            int8 [M, N/2]      y_scale      fp32 [M]
+ *   workspace    device bytes >= cb_grouped_matmul_swiglu_quant_workspace_size(M, K, N, E)
+ * M == 0, N == 0 or E == 0 returns CB_OK without a launch (gmsq_plugin.cpp:93-95).
+ */
+int64_t cb_grouped_matmul_swiglu_quant_workspace_size(int64_t M, int64_t K, int64_t N, int64_t E);
+int cb_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* weight, const float* weight_scale,
+                                   const float* x_scale, const int64_t* group_list,
+                                   int64_t group_len, int64_t M, int64_t K, int64_t N, int64_t E,
+                                   int8_t* y, float* y_scale, void* workspace,
+                                   int64_t workspace_bytes, void* stream);
+
+/*
+ * QuantMatmul (dense W8A8 with dequant epilogue).
+ * Replaces quant_matmul(Tensor x1, Tensor x2, Tensor scale, *, Tensor? offset=None,
+ *   Tensor? pertoken_scale=None, Tensor? bias=None, str? output_dtype=None) -> Tensor
+ * (operators/quantmatmul/csrc/ops/quant_matmul/op_plugin/quant_matmul_plugin.cpp:48-49,77-267)
+ * and qm_launch_cube_i32 + qm_launch_epilogue_{f16,bf16} (op_kernel/quant_matmul_launch.h:87-98).
+ *
+ *   x1 int8 [batch, M, K], x2 int8 [batch, K, N] (N contiguous), out [batch, M, N]
+ *   scale      : scale_dtype (fp32 / bf16), scale_numel 1 or N
+ *   offset     : fp32, offset_numel 0 (absent), 1 or N
+ *   pertoken   : fp32, pertoken_numel 0 (absent) or M (indexed by row modulo M)
+ *   bias       : bias_dtype (int32 / fp16 / bf16 / fp32), bias_numel 0 (absent), 1 or N,
+ *                or batch*N when bias_batched != 0 (a [batch, 1, N] bias)
+ *   out_dtype  : CB_DT_FLOAT16 (the reference's default) or CB_DT_BFLOAT16
+ *   out[b,m,n] = cast((float(c) (+ i32 bias)) * scale (+ offset) (* pertoken[m]) (+ float bias))
+ */
+int cb_quant_matmul(const int8_t* x1, const int8_t* x2, const void* scale, int scale_dtype,
+                    int64_t scale_numel, const float* offset, int64_t offset_numel,
+                    const float* pertoken, int64_t pertoken_numel, const void* bias, int bias_dtype,
+                    int64_t bias_numel, int bias_batched, int64_t batch, int64_t M, int64_t K,
+                    int64_t N, int out_dtype, void* out, void* stream);
+
+/*
+ * int8 grouped down-projection (W8A8 GroupedMatmul with a per-token x per-channel dequant to bf16).
+ * The reference has no int8 grouped matmul: the group semantics follow
+ * grouped_matmul(Tensor x, Tensor weight, int[] group_list, ...) with split_item = 2 (one joined
+ * output) (operators/groupedmatmul/csrc/ops/grouped_matmul/op_plugin/grouped_matmul_plugin.cpp:42-43,82-95)
+ * and the epilogue follows QuantMatmul's scale-then-pertoken order
+ * (operators/quantmatmul/csrc/ops/quant_matmul/op_kernel/quant_matmul_epilogue_kernel.cpp:273-292).
+ *
+ *   x int8 [M, K], weight int8 [E, K, N], weight_scale fp32 [E, N], x_scale fp32 [M]
+ *   out bf16 [M, N]:  out[i, n] = bf16((float(x[i] . weight[g(i)][:, n]) * weight_scale[g, n]) * x_scale[i])
+ */
+int cb_grouped_matmul_quant(const int8_t* x, const int8_t* weight, const float* weight_scale,
+                            const float* x_scale, const int64_t* group_list, int64_t group_len,
+                            int64_t M, int64_t K, int64_t N, int64_t E, void* out, void* stream);
+
+/*
+ * Raw grouped int8 GEMM with exact int32 accumulation: c[rows_g, :] = x[rows_g, :] @ weight[g].
+ * Replaces the reference's first GroupedMatmulSwigluQuant stage launch_gmsq_cube(x, w, c, ws, M, K,
+ * N, E, GmsqGroupArg, stream) (op_kernel/gmsq_launch.h:67-69, gmsq_cube_kernel.cpp:15-16), which
+ * writes the int32 [M, N] workspace its vector stage consumes.  Uses the same kernels as the fused
+ * operators, with an int32 store epilogue.
+ *   x int8 [M, K], weight int8 [E, K, N], c int32 [M, N]
+ */
+int cb_grouped_matmul_int32(const int8_t* x, const int8_t* weight, const int64_t* group_list,
+                            int64_t group_len, int64_t M, int64_t K, int64_t N, int64_t E, int32_t* c,
+                            void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CANNBENCH_AMD_H */

@@ -1,0 +1,124 @@
+"""C ABI checks that need no GPU: the library loads, exports every symbol include/cannbench_amd.h
+declares, and each entry point rejects bad arguments with the right status before touching a
+device (validation runs before any HIP call)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "cannbench_amd.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(cb_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib(cb):
+    from importlib import import_module
+    L = import_module("cannbench-operator-solutions_amd._lib")
+    return L, L.load()
+
+
+def test_header_symbols_exported(lib):
+    L, so = lib
+    syms = declared_symbols()
+    assert len(syms) >= 8
+    for s in syms:
+        assert hasattr(so, s), f"{s} declared in the header but not exported"
+        assert s in L.SIGNATURES, f"{s} has no ctypes signature"
+
+
+def test_version_and_status_strings(lib):
+    L, so = lib
+    assert b"gfx950" in so.cb_version()
+    assert L.status_string(L.CB_ERR_N_ODD) == "N must be even"
+    assert L.status_string(L.CB_ERR_GROUP_TOTAL) == "group_list[-1] must equal M"
+    assert L.status_string(999) == "unknown status"
+
+
+def _gl(vals):
+    return (ctypes.c_int64 * max(1, len(vals)))(*vals)
+
+
+FAKE = 0x1000  # a non-NULL pointer value; never dereferenced because validation fails first
+
+
+@pytest.mark.parametrize("gl,E,M,N,expect", [
+    ([4, 8], 2, 8, 7, "CB_ERR_N_ODD"),
+    ([4, 8], 3, 8, 8, "CB_ERR_GROUP_LEN"),
+    ([4, 3], 2, 8, 8, "CB_ERR_GROUP_ORDER"),
+    ([4, 9], 2, 8, 8, "CB_ERR_GROUP_ORDER"),
+    ([4, 7], 2, 8, 8, "CB_ERR_GROUP_TOTAL"),
+    ([1] * 257, 257, 1, 8, "CB_ERR_GROUP_COUNT"),
+    ([4, 8], 2, 0, 8, "CB_OK"),          # M == 0: early return, nothing launched
+])
+def test_gmsq_validation(lib, gl, E, M, N, expect):
+    L, so = lib
+    rc = so.cb_grouped_matmul_swiglu_quant(FAKE, FAKE, FAKE, FAKE, _gl(gl), len(gl), M, 64, N, E,
+                                           FAKE, FAKE, FAKE, 1 << 40, None)
+    assert rc == getattr(L, expect)
+
+
+def test_gmsq_workspace_checked(lib):
+    L, so = lib
+    M, K, N, E = 8, 64, 32, 2
+    need = so.cb_grouped_matmul_swiglu_quant_workspace_size(M, K, N, E)
+    assert need >= M * (N // 2) * 4 + M * 4
+    rc = so.cb_grouped_matmul_swiglu_quant(FAKE, FAKE, FAKE, FAKE, _gl([4, 8]), 2, M, K, N, E,
+                                           FAKE, FAKE, FAKE, need - 1, None)
+    assert rc == L.CB_ERR_WORKSPACE
+    rc = so.cb_grouped_matmul_swiglu_quant(FAKE, FAKE, FAKE, FAKE, _gl([4, 8]), 2, M, K, N, E,
+                                           FAKE, FAKE, None, need, None)
+    assert rc == L.CB_ERR_WORKSPACE
+
+
+def test_gmsq_null_pointer(lib):
+    L, so = lib
+    rc = so.cb_grouped_matmul_swiglu_quant(None, FAKE, FAKE, FAKE, _gl([8]), 1, 8, 64, 32, 1,
+                                           FAKE, FAKE, FAKE, 1 << 30, None)
+    assert rc == L.CB_ERR_NULL_POINTER
+
+
+@pytest.mark.parametrize("kw,expect", [
+    (dict(scale_dtype=5), "CB_ERR_DTYPE"),
+    (dict(out_dtype=3), "CB_ERR_DTYPE"),
+    (dict(K=0), "CB_ERR_EMPTY"),
+    (dict(scale_numel=7), "CB_ERR_SCALE_LEN"),
+    (dict(offset_numel=3), "CB_ERR_SCALE_LEN"),
+    (dict(pertoken_numel=5), "CB_ERR_SCALE_LEN"),
+    (dict(bias_numel=3, bias_dtype=3), "CB_ERR_SCALE_LEN"),
+    (dict(bias_numel=32, bias_dtype=4), "CB_ERR_DTYPE"),
+    (dict(bias_numel=64, bias_dtype=3, bias_batched=1, batch=1), "CB_ERR_SCALE_LEN"),
+])
+def test_quant_matmul_validation(lib, kw, expect):
+    L, so = lib
+    a = dict(scale_dtype=3, scale_numel=32, offset_numel=0, pertoken_numel=0, bias_numel=0, bias_dtype=3,
+             bias_batched=0, batch=1, M=16, K=64, N=32, out_dtype=2)
+    a.update(kw)
+    rc = so.cb_quant_matmul(FAKE, FAKE, FAKE, a["scale_dtype"], a["scale_numel"], FAKE, a["offset_numel"],
+                            FAKE, a["pertoken_numel"], FAKE, a["bias_dtype"], a["bias_numel"], a["bias_batched"],
+                            a["batch"], a["M"], a["K"], a["N"], a["out_dtype"], FAKE, None)
+    assert rc == getattr(L, expect)
+
+
+def test_grouped_matmul_quant_validation(lib):
+    L, so = lib
+    assert so.cb_grouped_matmul_quant(FAKE, FAKE, FAKE, FAKE, _gl([3, 2]), 2, 3, 64, 32, 2, FAKE, None) \
+        == L.CB_ERR_GROUP_ORDER
+    assert so.cb_grouped_matmul_quant(FAKE, FAKE, FAKE, FAKE, _gl([3]), 1, 3, 64, 32, 0, FAKE, None) \
+        == L.CB_ERR_GROUP_COUNT
+
+
+def test_norm_quant_validation(lib):
+    L, so = lib
+    assert so.cb_add_rms_norm_dynamic_quant(FAKE, FAKE, FAKE, 3, 4, 64, 1e-6, FAKE, FAKE, FAKE, None) == L.CB_ERR_DTYPE
+    assert so.cb_add_rms_norm_dynamic_quant(FAKE, FAKE, FAKE, 2, 4, 16385, 1e-6, FAKE, FAKE, FAKE, None) \
+        == L.CB_ERR_ROW_TOO_LONG
+    assert so.cb_add_rms_norm_dynamic_quant(FAKE, FAKE, FAKE, 2, 0, 64, 1e-6, FAKE, FAKE, FAKE, None) == L.CB_OK
+    assert so.cb_dynamic_quant(FAKE, 4, 4, 64, FAKE, FAKE, None) == L.CB_ERR_DTYPE
+    assert so.cb_dynamic_quant(FAKE, 1, 4, 0, FAKE, FAKE, None) == L.CB_ERR_EMPTY
