@@ -1,0 +1,240 @@
+"""Benchmark of the W8A8 MoE-FFN hot path on one MI355X.
+
+Headline (`value`): GroupedMatmulSwigluQuant on the prefill configuration (131072 int8 rows,
+256 experts, K 7168, N 4096, Zipf(1.1) routing), in TOPS = 2*M*K*N / wall time of the whole op
+(all of its kernels), inputs resident in HBM.  The same JSON line also carries the decode
+configuration (GB/s of algorithmic bytes), its down-projection, AddRmsNormDynamicQuant and the
+dense QuantMatmul, each with its own roofline figure, plus a CPU baseline (the C oracle on a
+bounded sample of the prefill rows, on the host cores).
+
+A step is one operator call over one batch of synthetic input.  Usage:
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only prefill,decode,...] [--no-cpu]
+"""
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+cb = importlib.import_module("cannbench-operator-solutions_amd")
+cfgs = importlib.import_module("cannbench-operator-solutions_amd.configs")
+L = importlib.import_module("cannbench-operator-solutions_amd._lib")
+
+METRIC = "GroupedMatmulSwigluQuant int8 TOPS (%MFMA peak) + decode HBM GB/s (%peak), 1 GPU"
+PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 MFMA, published
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, published
+
+
+class KernelTimer:
+    """HIP events around the main GEMM kernel of the next call (cb_set_kernel_timing), recorded on
+    the stream the kernel is launched on."""
+
+    def __init__(self, n):
+        self.pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        for a, b in self.pairs:  # materialise the underlying hipEvent_t handles
+            a.record()
+            b.record()
+        torch.cuda.synchronize()
+        self.i = 0
+
+    def arm(self):
+        a, b = self.pairs[self.i]
+        self.i += 1
+        L.load().cb_set_kernel_timing(a.cuda_event, b.cuda_event)
+
+    def mean_ms(self):
+        ts = [a.elapsed_time(b) for a, b in self.pairs[: self.i]]
+        return float(np.mean(ts)) if ts else None
+
+
+def time_op(fn, steps, warmup, timer=None):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        if timer is not None:
+            timer.arm()
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def roofline(bound, achieved, unit, traffic=None):
+    peak = PEAK_INT8_TOPS if bound == "mfma" else PEAK_HBM_GBS
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+# ------------------------------------------------------------------------------------------------
+def bench_prefill(steps, warmup, dev, keep):
+    d = cfgs.make_gmsq_prefill(dev)
+    M, K = d["x"].shape
+    N = d["weight"].shape[2]
+    ops = 2.0 * M * K * N
+    fn = lambda: cb.grouped_matmul_swiglu_quant(d["x"], d["weight"], d["weight_scale"], d["x_scale"], d["group_list"])
+    timer = KernelTimer(steps)
+    ms = time_op(fn, steps, warmup, timer)
+    kms = timer.mean_ms()
+    counts = np.diff([0] + d["group_list"])
+    res = {"ms": ms, "tops": ops / (ms * 1e-3) / 1e12, "gemm_kernel_ms": kms,
+           "roofline": roofline("mfma", ops / (kms * 1e-3) / 1e12, "TFLOP/s"),
+           "config": {"workload": "gmsq_prefill", "rows": M, "experts": len(counts), "K": K, "N": N,
+                      "routing": "zipf(1.1) multinomial, numpy seed 0",
+                      "rows_per_expert_max": int(counts.max()), "rows_per_expert_min": int(counts.min())}}
+    keep["prefill"] = d
+    return res
+
+
+def decode_bytes(counts, K, N):
+    M = int(np.sum(counts))
+    act = int(np.sum(np.asarray(counts) > 0))
+    return act * K * N + M * K + M * (N // 2) + 8 * M + 4 * N * act
+
+
+def bench_decode(steps, warmup, dev, keep):
+    d = cfgs.make_gmsq_decode(dev)
+    M, K = d["x"].shape
+    E, _, N = d["weight"].shape
+    counts = np.diff([0] + d["group_list"])
+    nbytes = decode_bytes(counts, K, N)
+    fn = lambda: cb.grouped_matmul_swiglu_quant(d["x"], d["weight"], d["weight_scale"], d["x_scale"], d["group_list"])
+    timer = KernelTimer(steps)
+    ms = time_op(fn, steps, warmup, timer)
+    kms = timer.mean_ms()
+    res = {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes, "gemm_kernel_ms": kms,
+           "roofline": roofline("hbm", nbytes / (kms * 1e-3) / 1e9, "GB/s"),
+           "config": {"workload": "gmsq_decode", "rows": M, "experts": E, "K": K, "N": N,
+                      "routing": "256 tokens x top-8 uniform, numpy seed 0",
+                      "rows_per_expert_max": int(counts.max()), "rows_per_expert_min": int(counts.min())}}
+    # down-projection on the decode output
+    y, ys = fn()
+    w2, ws2 = d["down_weight"], d["down_weight_scale"]
+    K2, N2 = w2.shape[1], w2.shape[2]
+    act_e = int(np.sum(counts > 0))
+    b2 = act_e * K2 * N2 + M * K2 + 2 * M * N2 + 4 * M + 4 * N2 * act_e
+    fn2 = lambda: cb.grouped_matmul_quant(y, w2, ws2, ys, d["group_list"])
+    timer2 = KernelTimer(steps)
+    ms2 = time_op(fn2, steps, warmup, timer2)
+    k2 = timer2.mean_ms()
+    down = {"ms": ms2, "gbs": b2 / (ms2 * 1e-3) / 1e9, "bytes": b2, "gemm_kernel_ms": k2,
+            "roofline": roofline("hbm", b2 / (k2 * 1e-3) / 1e9, "GB/s"),
+            "config": {"workload": "down_proj", "rows": M, "K": K2, "N": N2, "experts": E}}
+    return res, down
+
+
+def bench_ardq(steps, warmup, dev):
+    d = cfgs.make_ardq(dev)
+    R, H = d["x1"].shape
+    nbytes = 2 * (2 * R * H) + 2 * H + 2 * R * H + R * H + 4 * R
+    fn = lambda: cb.add_rms_norm_dynamic_quant(d["x1"], d["x2"], d["gamma"], d["epsilon"])
+    ms = time_op(fn, steps, warmup)
+    return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes,
+            "roofline": roofline("hbm", nbytes / (ms * 1e-3) / 1e9, "GB/s"),
+            "config": {"workload": "ardq", "rows": R, "cols": H, "dtype": "bf16"}}
+
+
+def bench_qmm(steps, warmup, dev):
+    d = cfgs.make_qmm(dev)
+    M, K = d["x1"].shape
+    N = d["x2"].shape[1]
+    ops = 2.0 * M * K * N
+    fn = lambda: cb.quant_matmul(d["x1"], d["x2"], d["scale"], pertoken_scale=d["pertoken_scale"],
+                                 output_dtype="bfloat16")
+    timer = KernelTimer(steps)
+    ms = time_op(fn, steps, warmup, timer)
+    kms = timer.mean_ms()
+    return {"ms": ms, "tops": ops / (ms * 1e-3) / 1e12, "gemm_kernel_ms": kms,
+            "roofline": roofline("mfma", ops / (kms * 1e-3) / 1e12, "TFLOP/s"),
+            "config": {"workload": "qmm", "M": M, "K": K, "N": N}}
+
+
+def cpu_baseline(d, budget_s=12.0):
+    """The C oracle on the host cores over whole experts of the prefill config, until ~budget_s."""
+    from oracle import oracle as orc
+    gl = d["group_list"]
+    starts = [0] + gl[:-1]
+    K = d["x"].shape[1]
+    N = d["weight"].shape[2]
+    ws = d["weight_scale"].cpu().numpy()
+    xs = d["x_scale"].cpu().numpy()
+    order = np.argsort([e - s for s, e in zip(starts, gl)])  # lightest experts first, then heavier
+    done_rows, t_total, experts = 0, 0.0, []
+    for g in order[len(order) // 2:]:
+        s, e = starts[g], gl[g]
+        if e == s:
+            continue
+        x = d["x"][s:e].cpu().numpy()
+        w = d["weight"][g:g + 1].cpu().numpy()
+        t0 = time.perf_counter()
+        orc.gmsq(x, w, ws[g:g + 1], xs[s:e], np.array([e - s]))
+        t_total += time.perf_counter() - t0
+        done_rows += e - s
+        experts.append(int(g))
+        if t_total >= budget_s:
+            break
+    ops = 2.0 * done_rows * K * N
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(ops / t_total / 1e12, 4), "unit": "TOPS", "cores": cores, "kind": "port",
+            "sample": f"oracle/cb_oracle.c or_gmsq (OpenMP) on {done_rows} rows = {len(experts)} whole experts "
+                      f"of the prefill config, {t_total:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--only", default="prefill,decode,ardq,qmm")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the operators are single-device; expert "
+              "parallelism across GPUs is a design note, not a measured path). Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm device visible", file=sys.stderr)
+        sys.exit(2)
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    only = set(args.only.split(","))
+    keep = {}
+    out = {"metric": METRIC, "value": None, "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "int8",
+           "data": "synthetic: seeded device-generated int8 / fp32 tensors, numpy-seeded routing"}
+    if "prefill" in only:
+        p = bench_prefill(args.steps, args.warmup, dev, keep)
+        out.update(value=round(p["tops"], 2), ms_per_step=round(p["ms"], 4), config=p["config"],
+                   roofline=p["roofline"])
+        out["prefill_gemm_kernel_ms"] = round(p["gemm_kernel_ms"], 4)
+        out["frac_of_int8_peak"] = round(p["tops"] / PEAK_INT8_TOPS, 4)
+    if "decode" in only:
+        keep.pop("prefill_tensors", None)
+        dres, down = bench_decode(args.steps, args.warmup, dev, keep)
+        out["decode"] = {"value": round(dres["gbs"], 1), "unit": "GB/s", "ms_per_step": round(dres["ms"], 4),
+                         "frac_of_hbm_peak": round(dres["gbs"] / PEAK_HBM_GBS, 4), "bytes": dres["bytes"],
+                         "roofline": dres["roofline"], "config": dres["config"]}
+        out["down_proj"] = {"value": round(down["gbs"], 1), "unit": "GB/s", "ms_per_step": round(down["ms"], 4),
+                            "bytes": down["bytes"], "roofline": down["roofline"], "config": down["config"]}
+    if "ardq" in only:
+        a = bench_ardq(args.steps, args.warmup, dev)
+        out["ardq"] = {"value": round(a["gbs"], 1), "unit": "GB/s", "ms_per_step": round(a["ms"], 4),
+                       "roofline": a["roofline"], "config": a["config"]}
+    if "qmm" in only:
+        q = bench_qmm(args.steps, args.warmup, dev)
+        out["qmm"] = {"value": round(q["tops"], 2), "unit": "TOPS", "ms_per_step": round(q["ms"], 4),
+                      "roofline": q["roofline"], "config": q["config"]}
+    if not args.no_cpu and "prefill" in keep:
+        out["cpu_baseline"] = cpu_baseline(keep["prefill"])
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

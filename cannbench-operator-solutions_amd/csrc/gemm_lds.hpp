@@ -1,0 +1,329 @@
+// gemm_lds.hpp - the prefill / dense int8 GEMM core: direct-to-LDS loads + transposing LDS reads.
+//
+// Tile 256 (rows) x 256 (weight columns) x 64 (K), STAGES-deep LDS ring.  Global -> LDS traffic
+// uses buffer_load_dwordx4 ... lds (each lane's 16 bytes land at lane-linear LDS addresses, no
+// VGPR staging).  Both tiles keep their HBM layout in LDS and are XOR-swizzled at 16-byte
+// granularity by choosing which global chunk each lane fetches:
+//   A tile [256][64] (K contiguous, 64-byte rows):  position p of row r holds k-chunk p ^ ((r >> 2) & 3)
+//   B tile [64][256] (N contiguous, 256-byte rows): position p of row k holds column chunk
+//                                                   p ^ ((k & 7) << 1)
+// MFMA v_mfma_i32_32x32x32_i8 operands:
+//   A: ds_read_b128 of 16 consecutive K bytes of one row.
+//   B: two ds_read_b64_tr_b8 per operand.  Within each group of 16 lanes the instruction returns
+//      to lane i byte j the byte (i & 7) of the 8 bytes read by lane 2 j + (i >> 3); lane s of a
+//      group therefore reads row kb + (s >> 1), columns c0 + 8 (s & 1) .. +8, and lane i receives
+//      8 consecutive K values of column c0 + i: the weight is transposed by the LDS read itself.
+// The swizzles make every 16-lane phase of those reads touch 16 distinct 16-byte bank groups.
+#pragma once
+
+#include <type_traits>
+
+#include "gemm_i8.hpp"
+
+namespace cb {
+
+typedef int v2i __attribute__((ext_vector_type(2)));
+#define CB_LDS __attribute__((address_space(3)))
+
+// The LDS DMA and the stage barrier are written as inline asm on purpose: when the compiler sees
+// buffer_load ... lds it must assume every later LDS read may alias the DMA target and waits for
+// vmcnt(0), and a __syncthreads() fence also drains vmcnt - either would serialise the stage
+// pipeline.  The waits below are explicit instead: before stage kt is read, each wave waits until
+// only the DMAs of later stages are outstanding, then the barrier publishes every wave's stage.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t lds_addr)
+{
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc),
+                 "s"(lds_addr)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_barrier()
+{
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+template <int WM, int WN, int STAGES>
+struct LdsCfg {
+    static constexpr int BM = 256, BN = 256, BK = 64;
+    static constexpr int NW = WM * WN, NT = 64 * NW;
+    static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+    static constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN, STAGE = A_BYTES + B_BYTES;
+    static constexpr int LDS_BYTES = STAGES * STAGE;
+    static constexpr int A_ISSUE = A_BYTES / 16 / NT;  // DMA instructions per thread per stage
+    static constexpr int B_ISSUE = B_BYTES / 16 / NT;
+    static constexpr int ISSUE = A_ISSUE + B_ISSUE;
+    static_assert(A_ISSUE >= 1 && B_ISSUE >= 1, "tile too small for the workgroup");
+    static_assert(FN >= 2 && FN % 2 == 0, "wave tile must hold gate/up pairs");
+};
+
+template <int EPI, int WM, int WN, int STAGES>
+__global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArgs a)
+{
+    using C = LdsCfg<WM, WN, STAGES>;
+    constexpr int BM = C::BM, BN = C::BN, BK = C::BK, NW = C::NW, TM = C::TM, TN = C::TN, FM = C::FM,
+                  FN = C::FN;
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    const int64_t K = a.K, N = a.N;
+    const EpiArgs& e = a.epi;
+    const int64_t b = blockIdx.y;
+
+    // ---- tile selection (XCD remap + GROUP_M swizzle) -------------------------------------
+    const int pid = xcd_remap(blockIdx.x, gridDim.x);
+    constexpr int GROUP_M = 4;
+    const int T_m = a.gt.total_mtiles, T_n = a.ntiles;
+    const int per_group = GROUP_M * T_n;
+    const int gid = pid / per_group;
+    const int first_m = gid * GROUP_M;
+    const int gsz = (T_m - first_m) < GROUP_M ? (T_m - first_m) : GROUP_M;
+    const int mt = first_m + (pid % per_group) % gsz;
+    const int nt = (pid % per_group) / gsz;
+
+    const int g = group_of_tile(a.gt, mt);
+    const int rs = g ? a.gt.row_end[g - 1] : 0;
+    const int r1 = a.gt.row_end[g];
+    const int m0 = rs + (mt - a.gt.tile_start[g]) * BM;
+    const int vrows = r1 - m0;  // valid rows of this tile (>= 1)
+
+    // buffer resources: A = rows [m0, r1) of x, B = this group's weight [K, N]
+    const __amdgpu_buffer_rsrc_t ares =
+        make_rsrc(a.x + b * a.x_bstride + (int64_t)m0 * K, (uint32_t)((int64_t)vrows * K));
+    const __amdgpu_buffer_rsrc_t bres =
+        make_rsrc(a.w + b * a.w_bstride + (int64_t)g * a.w_gstride, (uint32_t)(K * N));
+
+    // ---- per-lane DMA source offsets (stage independent part) -----------------------------
+    uint32_t a_off[C::A_ISSUE];
+#pragma unroll
+    for (int i = 0; i < C::A_ISSUE; ++i) {
+        const int cid = (i * NW + wave) * 64 + lane;  // 16-byte chunk id in the A tile
+        const int row = cid >> 2, pos = cid & 3;
+        const int q = pos ^ ((row >> 2) & 3);
+        const int rr = row < vrows ? row : vrows - 1;
+        a_off[i] = (uint32_t)rr * (uint32_t)K + (uint32_t)(q * 16);
+    }
+    uint32_t b_off[C::B_ISSUE];
+#pragma unroll
+    for (int i = 0; i < C::B_ISSUE; ++i) {
+        const int cid = (i * NW + wave) * 64 + lane;
+        const int row = cid >> 4, pos = cid & 15;
+        const int c = pos ^ ((row & 7) << 1);  // logical 16-column chunk
+        int64_t col;
+        bool ok;
+        if constexpr (EPI == EPI_SWIGLU) {
+            const int64_t j = (int64_t)nt * (BN / 2) + 16 * (c & 7);
+            ok = j < e.H;
+            col = c < 8 ? j : e.H + j;
+        } else {
+            col = (int64_t)nt * BN + 16 * c;
+            ok = col < N;
+        }
+        b_off[i] = (uint32_t)row * (uint32_t)N + (uint32_t)(ok ? col : 0);
+    }
+
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(CB_LDS uint8_t*)smem;
+    auto issue_stage = [&](int kt) {
+        const uint32_t sa = lds_base + (uint32_t)((kt % STAGES) * C::STAGE);
+        const uint32_t sb = sa + C::A_BYTES;
+        const uint32_t ka = (uint32_t)(kt * BK);
+        const uint32_t kb = (uint32_t)(kt * BK) * (uint32_t)N;
+#pragma unroll
+        for (int i = 0; i < C::A_ISSUE; ++i)
+            dma16(ares, a_off[i] + ka, __builtin_amdgcn_readfirstlane(sa + (uint32_t)((i * NW + wave) * 1024)));
+#pragma unroll
+        for (int i = 0; i < C::B_ISSUE; ++i)
+            dma16(bres, b_off[i] + kb, __builtin_amdgcn_readfirstlane(sb + (uint32_t)((i * NW + wave) * 1024)));
+    };
+
+    auto tcol = [&](int fn) -> int {  // first tile column of wave fragment fn
+        if constexpr (EPI == EPI_SWIGLU)
+            return fn < FN / 2 ? wn * (TN / 2) + fn * 32 : BN / 2 + wn * (TN / 2) + (fn - FN / 2) * 32;
+        else
+            return wn * TN + fn * 32;
+    };
+
+    // ---- per-lane LDS read offsets ----------------------------------------------------------
+    // A: fragment fm of wave row wm covers tile rows 32 (WM fm + wm) .. +32 (row blocks are
+    // interleaved over the WM waves so a partial tile loads them evenly); lane % 32 picks the row,
+    // k-chunk q = 2 ks + lane / 32
+    uint32_t a_rd[FM][2];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+        const int r = (WM * fm + wm) * 32 + (lane & 31);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int q = 2 * ks + (lane >> 5);
+            a_rd[fm][ks] = (uint32_t)(r * BK + ((q ^ ((r >> 2) & 3)) << 4));
+        }
+    }
+    // B: group gq = lane / 16 -> k half (gq >> 1), column half (gq & 1); in-group lane s -> row
+    // offset s >> 1, byte half s & 1
+    const int gq = lane >> 4, s = lane & 15;
+    uint32_t b_rd[FN][2][2];  // [fn][ks][low/high 8 k]
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+        const int cc = (tcol(fn) >> 4) + (gq & 1);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const int row = ks * 32 + (gq >> 1) * 16 + hf * 8 + (s >> 1);
+                const int pos = cc ^ ((row & 7) << 1);
+                b_rd[fn][ks][hf] = (uint32_t)(C::A_BYTES + row * BN + pos * 16 + (s & 1) * 8);
+            }
+        }
+    }
+
+    // 32-row fragments of this wave that hold valid rows (wave-uniform); tiles at a group's end run
+    // a loop variant without the MFMAs of the empty fragments
+    const int nblk = (vrows + 31) / 32;
+    const int nvf = __builtin_amdgcn_readfirstlane(nblk > wm ? ((nblk - wm + WM - 1) / WM > FM ? FM : (nblk - wm + WM - 1) / WM) : 0);
+
+    v16i acc[FM][FN];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0;
+
+    const int nk = (int)((K + BK - 1) / BK);
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st)
+        if (st < nk) issue_stage(st);
+
+    auto kloop = [&](auto nv_const) {
+        constexpr int NV = decltype(nv_const)::value;  // fragments that get MFMAs
+        for (int kt = 0; kt < nk; ++kt) {
+            // own DMAs for stage kt done (later stages may stay in flight), then everyone's
+            const int ahead = nk - 1 - kt < STAGES - 2 ? nk - 1 - kt : STAGES - 2;
+            static_assert(STAGES >= 2 && STAGES <= 5, "wait chain below covers up to 3 stages ahead");
+            if (STAGES >= 5 && ahead >= 3) wait_vmcnt_barrier<3 * C::ISSUE>();
+            else if (STAGES >= 4 && ahead >= 2) wait_vmcnt_barrier<2 * C::ISSUE>();
+            else if (STAGES >= 3 && ahead >= 1) wait_vmcnt_barrier<C::ISSUE>();
+            else wait_vmcnt_barrier<0>();
+            if (kt + STAGES - 1 < nk) issue_stage(kt + STAGES - 1);
+            if constexpr (NV > 0) {
+                const CB_LDS uint8_t* base = (const CB_LDS uint8_t*)smem + (kt % STAGES) * C::STAGE;
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    v4i af[NV], bf[FN];
+#pragma unroll
+                    for (int fm = 0; fm < NV; ++fm) af[fm] = *(const CB_LDS v4i*)(base + a_rd[fm][ks]);
+#pragma unroll
+                    for (int fn = 0; fn < FN; ++fn) {
+                        const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((CB_LDS v2i*)(base + b_rd[fn][ks][0]));
+                        const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((CB_LDS v2i*)(base + b_rd[fn][ks][1]));
+                        bf[fn] = v4i{lo[0], lo[1], hi[0], hi[1]};
+                    }
+#pragma unroll
+                    for (int fm = 0; fm < NV; ++fm)
+#pragma unroll
+                        for (int fn = 0; fn < FN; ++fn)
+                            acc[fm][fn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[fm], bf[fn], acc[fm][fn], 0, 0, 0);
+                }
+            }
+        }
+    };
+    static_assert(FM <= 4, "loop variants below cover up to 4 fragments");
+    if (nvf >= FM) kloop(std::integral_constant<int, FM>());
+    else if (FM > 3 && nvf == 3) kloop(std::integral_constant<int, (FM > 3 ? 3 : 0)>());
+    else if (FM > 2 && nvf == 2) kloop(std::integral_constant<int, (FM > 2 ? 2 : 0)>());
+    else if (FM > 1 && nvf == 1) kloop(std::integral_constant<int, (FM > 1 ? 1 : 0)>());
+    else kloop(std::integral_constant<int, 0>());
+
+    bool fvalid[FM];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) fvalid[fm] = fm < nvf;
+
+    // ---- epilogue.  32x32 C layout: lane l holds column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4
+    const int lr = (lane >> 5) * 4;
+    if constexpr (EPI == EPI_SWIGLU) {
+        const int64_t H = e.H;
+        float wsg[FN / 2], wsu[FN / 2];
+        int64_t jc[FN / 2];
+        bool jok[FN / 2];
+#pragma unroll
+        for (int fn = 0; fn < FN / 2; ++fn) {
+            jc[fn] = (int64_t)nt * (BN / 2) + wn * (TN / 2) + fn * 32 + (lane & 31);
+            jok[fn] = jc[fn] < H;
+            wsg[fn] = jok[fn] ? e.w_scale[(int64_t)g * N + jc[fn]] : 0.0f;
+            wsu[fn] = jok[fn] ? e.w_scale[(int64_t)g * N + H + jc[fn]] : 0.0f;
+        }
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) {
+            if (!fvalid[fm]) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + (WM * fm + wm) * 32 + (r >> 2) * 8 + lr + (r & 3);
+                const bool rowok = row < r1;
+                const float xs = rowok ? e.x_scale[row] : 0.0f;
+                float m = 0.0f;
+#pragma unroll
+                for (int fn = 0; fn < FN / 2; ++fn) {
+                    if (rowok && jok[fn]) {
+                        const float v = swiglu((float)acc[fm][fn][r], (float)acc[fm][fn + FN / 2][r], xs,
+                                               wsg[fn], wsu[fn]);
+                        e.act[(int64_t)row * H + jc[fn]] = v;
+                        m = fmaxf(m, fabsf(v));
+                    }
+                }
+#pragma unroll
+                for (int o = 1; o < 32; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+                if ((lane & 31) == 0 && rowok) atomicMax(e.amax + row, __float_as_uint(m));
+            }
+        }
+    } else if constexpr (EPI == EPI_I32) {
+        int32_t* ob = (int32_t*)e.out + b * e.out_bstride;
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) {
+            if (!fvalid[fm]) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + (WM * fm + wm) * 32 + (r >> 2) * 8 + lr + (r & 3);
+                if (row >= r1) continue;
+#pragma unroll
+                for (int fn = 0; fn < FN; ++fn) {
+                    const int64_t col = (int64_t)nt * BN + wn * TN + fn * 32 + (lane & 31);
+                    if (col < N) ob[(int64_t)row * N + col] = acc[fm][fn][r];
+                }
+            }
+        }
+    } else {
+        ColDeq cd[FN];
+        int64_t cc[FN];
+        bool cok[FN];
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+            cc[fn] = (int64_t)nt * BN + wn * TN + fn * 32 + (lane & 31);
+            cok[fn] = cc[fn] < N;
+            cd[fn] = col_deq(e, g, b, cok[fn] ? cc[fn] : 0);
+        }
+        uint16_t* ob = (uint16_t*)e.out + b * e.out_bstride;
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm) {
+            if (!fvalid[fm]) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + (WM * fm + wm) * 32 + (r >> 2) * 8 + lr + (r & 3);
+                if (row >= r1) continue;
+                const float pt = e.has_pt ? e.pertoken[row % e.pt_mod] : 1.0f;
+#pragma unroll
+                for (int fn = 0; fn < FN; ++fn) {
+                    if (cok[fn]) {
+                        const float v = apply_deq(e, cd[fn], acc[fm][fn][r], pt);
+                        ob[(int64_t)row * N + cc[fn]] = e.out_bf16 ? f32_to_bf16(v) : f32_to_f16(v);
+                    }
+                }
+            }
+        }
+    }
+}
+
+}  // namespace cb

@@ -6,7 +6,7 @@
 // enqueues its kernels on the caller's stream without any allocation or host synchronisation.
 #include <cstring>
 
-#include "gemm_i8.hpp"
+#include "gemm_lds.hpp"
 
 namespace cb {
 
@@ -74,10 +74,46 @@ static constexpr int kTiledBM = 128;
 #define CB_SKINNY_PREFETCH 1
 #endif
 static constexpr bool kSkinnyPrefetch = CB_SKINNY_PREFETCH;
+#ifndef CB_LDS_CORE
+#define CB_LDS_CORE 1
+#endif
+#ifndef CB_LDS_WM
+#define CB_LDS_WM 2
+#endif
+#ifndef CB_LDS_WN
+#define CB_LDS_WN 2
+#endif
+#ifndef CB_LDS_STAGES
+#define CB_LDS_STAGES 4
+#endif
+static constexpr bool kUseLdsCore = CB_LDS_CORE;
+static constexpr int kLdsWM = CB_LDS_WM, kLdsWN = CB_LDS_WN, kLdsStages = CB_LDS_STAGES;
+
+// Optional per-thread instrumentation: events recorded around the next main GEMM kernel launch
+// (set by cb_set_kernel_timing, consumed and cleared by that launch).
+struct KernelTiming {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+static thread_local KernelTiming g_timing;
+
+struct TimedLaunch {
+    hipStream_t st;
+    KernelTiming t;
+    explicit TimedLaunch(hipStream_t s) : st(s), t(g_timing)
+    {
+        g_timing = KernelTiming();
+        if (t.start) (void)hipEventRecord(t.start, st);
+    }
+    ~TimedLaunch()
+    {
+        if (t.stop) (void)hipEventRecord(t.stop, st);
+    }
+};
 
 template <int EPI>
 static void launch_gemm(GemmArgs& a, const int64_t* gl, int64_t E, int64_t batch, bool fast, hipStream_t st)
 {
+    TimedLaunch timed(st);
     const int64_t Ncols = (EPI == EPI_SWIGLU) ? a.epi.H : a.N;  // output columns
     build_group_table(a.gt, gl, E, kTiledBM);
     if (!fast) {
@@ -98,6 +134,19 @@ static void launch_gemm(GemmArgs& a, const int64_t* gl, int64_t E, int64_t batch
         return;
     }
     a.ntiles = (int)((EPI == EPI_SWIGLU) ? (Ncols + 127) / 128 : (Ncols + 255) / 256);
+    if (kUseLdsCore) {
+        using Cfg = LdsCfg<kLdsWM, kLdsWN, kLdsStages>;
+        build_group_table(a.gt, gl, E, Cfg::BM);
+        const int64_t blocks = (int64_t)a.gt.total_mtiles * a.ntiles;
+        auto kern = lds_gemm_kernel<EPI, kLdsWM, kLdsWN, kLdsStages>;
+        static bool attr_set = false;  // per template instance; idempotent, so a benign race
+        if (!attr_set) {
+            (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS_BYTES);
+            attr_set = true;
+        }
+        hipLaunchKernelGGL(kern, dim3((unsigned)blocks, (unsigned)batch), dim3(Cfg::NT), Cfg::LDS_BYTES, st, a);
+        return;
+    }
     const int64_t blocks = (int64_t)a.gt.total_mtiles * a.ntiles;
     const dim3 grid((unsigned)blocks, (unsigned)batch);
     hipLaunchKernelGGL((tiled_kernel<EPI, kTiledBM, 2>), grid, dim3(256), 0, st, a);
@@ -131,6 +180,12 @@ extern "C" const char* cb_status_string(int s)
 }
 
 extern "C" const char* cb_version(void) { return "cannbench_amd 0.1 gfx950"; }
+
+extern "C" void cb_set_kernel_timing(void* start_event, void* stop_event)
+{
+    g_timing.start = (hipEvent_t)start_event;
+    g_timing.stop = (hipEvent_t)stop_event;
+}
 
 extern "C" int64_t cb_grouped_matmul_swiglu_quant_workspace_size(int64_t M, int64_t K, int64_t N, int64_t E)
 {

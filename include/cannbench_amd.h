@@ -72,6 +72,14 @@ const char* cb_status_string(int status);
 const char* cb_version(void);
 
 /*
+ * Instrumentation (no reference counterpart): the next grouped / dense GEMM kernel launched by
+ * this thread through any entry point records hipEvent_t `start_event` before and `stop_event`
+ * after its main GEMM kernel on the call's stream, so a caller can time that kernel alone.
+ * The setting is consumed by that launch.  Either event may be NULL.
+ */
+void cb_set_kernel_timing(void* start_event, void* stop_event);
+
+/*
  * AddRmsNormDynamicQuant.
  * Replaces add_rms_norm_dynamic_quant(Tensor x1, Tensor x2, Tensor gamma, float epsilon)
  *   -> (Tensor y, Tensor xOut, Tensor scaleOut)
