@@ -7,7 +7,8 @@ import ctypes
 import os
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PKG_DIR, "libcannbench_amd.so")
+# CANNBENCH_AMD_LIB points at an alternative build of the same library (kernel tuning sweeps)
+LIB_PATH = os.environ.get("CANNBENCH_AMD_LIB") or os.path.join(PKG_DIR, "libcannbench_amd.so")
 
 # Status codes (cb_status in include/cannbench_amd.h).
 CB_OK = 0

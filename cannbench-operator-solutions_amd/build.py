@@ -31,9 +31,9 @@ def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-def _compile(src):
-    obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *HIP_FLAGS, "-c", src, "-o", obj]
+def _compile(src, defines=(), obj_dir=OBJ_DIR):
+    obj = os.path.join(obj_dir, os.path.basename(src) + ".o")
+    cmd = [HIPCC, *HIP_FLAGS, *[f"-D{d}" for d in defines], "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     msgs = [ln for ln in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in ln]
     if r.returncode != 0:
@@ -41,23 +41,24 @@ def _compile(src):
     return obj, msgs
 
 
-def build(verbose=False):
-    os.makedirs(OBJ_DIR, exist_ok=True)
+def build(verbose=False, defines=(), out=LIB_PATH, obj_dir=OBJ_DIR):
+    """Compile and link; `defines` are extra -D flags (tuning variants), `out` the library path."""
+    os.makedirs(obj_dir, exist_ok=True)
     srcs = sources()
     with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        results = list(ex.map(_compile, srcs))
+        results = list(ex.map(lambda s: _compile(s, defines, obj_dir), srcs))
     objs = [o for o, _ in results]
     if verbose:
         for _, msgs in results:
             for m in msgs:
                 print(m)
-    tmp = LIB_PATH + ".tmp"
+    tmp = out + ".tmp"
     cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":

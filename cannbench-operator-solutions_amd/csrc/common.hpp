@@ -44,6 +44,9 @@ __device__ __forceinline__ uint16_t f32_to_f16(float f)
     return __builtin_bit_cast(uint16_t, x);
 }
 
+// Hardware fp32 -> bf16 (v_cvt_pk_bf16_f32, round-half-even) for finite values.
+__device__ __forceinline__ uint16_t f32_to_bf16_hw(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+
 template <bool BF16>
 __device__ __forceinline__ float ld16(uint16_t h) { return BF16 ? bf16_to_f32(h) : f16_to_f32(h); }
 

@@ -119,11 +119,14 @@ __device__ __forceinline__ float apply_deq(const EpiArgs& e, const ColDeq& d, in
     return v;
 }
 
+// silu(L) * R with L, R the dequantised gate / up values.  exp and the division use the hardware
+// v_exp_f32 / v_rcp_f32 (about 1 ulp each), as the reference's vector unit does with its Exp and
+// Div (gmsq_vec_kernel.cpp:213-218); the int8 result moves by at most one rounding step.
 __device__ __forceinline__ float swiglu(float gate_c, float up_c, float xs, float wsg, float wsu)
 {
     const float L = (gate_c * xs) * wsg;
     const float R = (up_c * xs) * wsu;
-    return (L / (1.0f + expf(-L))) * R;
+    return (L * __builtin_amdgcn_rcpf(1.0f + __expf(-L))) * R;
 }
 
 __device__ __forceinline__ uint4 zero4() { return make_uint4(0u, 0u, 0u, 0u); }

@@ -23,6 +23,7 @@
 namespace cb {
 
 typedef int v2i __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 #define CB_LDS __attribute__((address_space(3)))
 
 // The LDS DMA and the stage barrier are written as inline asm on purpose: when the compiler sees
@@ -40,10 +41,14 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff
 }
 #pragma clang diagnostic pop
 
+// Workgroup barrier after the main loop: every wave's LDS reads are drained, so the stage buffers
+// can be reused for the epilogue staging.
+__device__ __forceinline__ void epi_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt_barrier()
 {
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
 template <int WM, int WN, int STAGES>
@@ -52,7 +57,11 @@ struct LdsCfg {
     static constexpr int NW = WM * WN, NT = 64 * NW;
     static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
     static constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN, STAGE = A_BYTES + B_BYTES;
-    static constexpr int LDS_BYTES = STAGES * STAGE;
+    // epilogue staging of the finished tile: 256 rows x 512 bytes (bf16 [256][256] or fp32
+    // [256][128]) with a 16-byte row pad that keeps rows 4 apart off the same banks
+    static constexpr int EPI_PITCH = 528;
+    static constexpr int EPI_BYTES = BM * EPI_PITCH;
+    static constexpr int LDS_BYTES = STAGES * STAGE > EPI_BYTES ? STAGES * STAGE : EPI_BYTES;
     static constexpr int A_ISSUE = A_BYTES / 16 / NT;  // DMA instructions per thread per stage
     static constexpr int B_ISSUE = B_BYTES / 16 / NT;
     static constexpr int ISSUE = A_ISSUE + B_ISSUE;
@@ -64,7 +73,7 @@ template <int EPI, int WM, int WN, int STAGES>
 __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArgs a)
 {
     using C = LdsCfg<WM, WN, STAGES>;
-    constexpr int BM = C::BM, BN = C::BN, BK = C::BK, NW = C::NW, TM = C::TM, TN = C::TN, FM = C::FM,
+    constexpr int BM = C::BM, BN = C::BN, BK = C::BK, NW = C::NW, TN = C::TN, FM = C::FM,
                   FN = C::FN;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
 
@@ -194,41 +203,80 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
             for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0;
 
     const int nk = (int)((K + BK - 1) / BK);
+    // Prologue: every LDS buffer gets a stage in flight.
 #pragma unroll
-    for (int st = 0; st < STAGES - 1; ++st)
+    for (int st = 0; st < STAGES; ++st)
         if (st < nk) issue_stage(st);
 
+    // Wait until stage `kt` is in LDS for every wave: own DMAs of stages after kt may stay in
+    // flight (`later` of them), own LDS reads are drained (the buffer about to be refilled was
+    // read by them), then the workgroup barrier.
+    auto wait_stage = [&](int later) {
+        static_assert(STAGES >= 2 && STAGES <= 5, "wait chain below covers up to 4 later stages");
+        if (STAGES >= 5 && later >= 4) wait_vmcnt_barrier<4 * C::ISSUE>();
+        else if (STAGES >= 4 && later >= 3) wait_vmcnt_barrier<3 * C::ISSUE>();
+        else if (STAGES >= 4 && later >= 2) wait_vmcnt_barrier<2 * C::ISSUE>();
+        else if (STAGES >= 3 && later >= 1) wait_vmcnt_barrier<C::ISSUE>();
+        else wait_vmcnt_barrier<0>();
+    };
+
+    // Software pipeline per stage kt (fragments of half-stage ks = 0 already in registers):
+    //   read ks = 1 fragments | MFMAs on ks = 0 | barrier for stage kt + 1, refill buffer of kt,
+    //   read kt + 1 ks = 0 fragments | MFMAs on ks = 1
+    // so LDS read latency hides behind MFMAs and the barrier sits between two MFMA groups.
     auto kloop = [&](auto nv_const) {
         constexpr int NV = decltype(nv_const)::value;  // fragments that get MFMAs
-        for (int kt = 0; kt < nk; ++kt) {
-            // own DMAs for stage kt done (later stages may stay in flight), then everyone's
-            const int ahead = nk - 1 - kt < STAGES - 2 ? nk - 1 - kt : STAGES - 2;
-            static_assert(STAGES >= 2 && STAGES <= 5, "wait chain below covers up to 3 stages ahead");
-            if (STAGES >= 5 && ahead >= 3) wait_vmcnt_barrier<3 * C::ISSUE>();
-            else if (STAGES >= 4 && ahead >= 2) wait_vmcnt_barrier<2 * C::ISSUE>();
-            else if (STAGES >= 3 && ahead >= 1) wait_vmcnt_barrier<C::ISSUE>();
-            else wait_vmcnt_barrier<0>();
-            if (kt + STAGES - 1 < nk) issue_stage(kt + STAGES - 1);
+        v4i a0[NV > 0 ? NV : 1], b0[FN], a1[NV > 0 ? NV : 1], b1[FN];
+        auto load = [&](int kt, int ks, v4i (&af)[NV > 0 ? NV : 1], v4i (&bf)[FN]) {
             if constexpr (NV > 0) {
                 const CB_LDS uint8_t* base = (const CB_LDS uint8_t*)smem + (kt % STAGES) * C::STAGE;
+#ifndef CB_ABLATE_NO_LDSREAD
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    v4i af[NV], bf[FN];
+                for (int fm = 0; fm < NV; ++fm) af[fm] = *(const CB_LDS v4i*)(base + a_rd[fm][ks]);
 #pragma unroll
-                    for (int fm = 0; fm < NV; ++fm) af[fm] = *(const CB_LDS v4i*)(base + a_rd[fm][ks]);
-#pragma unroll
-                    for (int fn = 0; fn < FN; ++fn) {
-                        const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((CB_LDS v2i*)(base + b_rd[fn][ks][0]));
-                        const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((CB_LDS v2i*)(base + b_rd[fn][ks][1]));
-                        bf[fn] = v4i{lo[0], lo[1], hi[0], hi[1]};
-                    }
-#pragma unroll
-                    for (int fm = 0; fm < NV; ++fm)
-#pragma unroll
-                        for (int fn = 0; fn < FN; ++fn)
-                            acc[fm][fn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[fm], bf[fn], acc[fm][fn], 0, 0, 0);
+                for (int fn = 0; fn < FN; ++fn) {
+                    const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((CB_LDS v2i*)(base + b_rd[fn][ks][0]));
+                    const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((CB_LDS v2i*)(base + b_rd[fn][ks][1]));
+                    bf[fn] = v4i{lo[0], lo[1], hi[0], hi[1]};
                 }
+#else
+#pragma unroll
+                for (int fm = 0; fm < NV; ++fm) af[fm] = v4i{kt, ks, fm, lane};
+#pragma unroll
+                for (int fn = 0; fn < FN; ++fn) bf[fn] = v4i{fn, kt, lane, ks};
+#endif
             }
+        };
+        auto mma = [&](const v4i (&af)[NV > 0 ? NV : 1], const v4i (&bf)[FN]) {
+            if constexpr (NV > 0) {
+#ifndef CB_ABLATE_NO_MFMA
+#pragma unroll
+                for (int fm = 0; fm < NV; ++fm)
+#pragma unroll
+                    for (int fn = 0; fn < FN; ++fn)
+                        acc[fm][fn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[fm], bf[fn], acc[fm][fn], 0, 0, 0);
+#else
+#pragma unroll
+                for (int fm = 0; fm < NV; ++fm)
+#pragma unroll
+                    for (int fn = 0; fn < FN; ++fn) acc[fm][fn][0] ^= af[fm][0] ^ bf[fn][1];
+#endif
+            }
+        };
+        wait_stage(nk - 1 < STAGES - 1 ? nk - 1 : STAGES - 1);
+        load(0, 0, a0, b0);
+        for (int kt = 0; kt < nk; ++kt) {
+            load(kt, 1, a1, b1);
+            mma(a0, b0);
+            if (kt + 1 < nk) {
+                const int later = nk - kt - 2 < STAGES - 2 ? nk - kt - 2 : STAGES - 2;
+                wait_stage(later);
+#ifndef CB_ABLATE_NO_DMA
+                if (kt + STAGES < nk) issue_stage(kt + STAGES);
+#endif
+                load(kt + 1, 0, a0, b0);
+            }
+            mma(a1, b1);
         }
     };
     static_assert(FM <= 4, "loop variants below cover up to 4 fragments");
@@ -242,43 +290,74 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) fvalid[fm] = fm < nvf;
 
+#ifdef CB_ABLATE_NO_EPI
+    {
+        int sum = 0;
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sum += acc[fm][fn][r];
+        if (sum == 0x7654321) ((int*)e.out)[tid] = sum;
+        return;
+    }
+#endif
     // ---- epilogue.  32x32 C layout: lane l holds column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4
     const int lr = (lane >> 5) * 4;
     if constexpr (EPI == EPI_SWIGLU) {
+        // act tile [256 rows][128 act columns] fp32 staged in LDS, then written with 16-byte stores
+        // and one row-max atomic per (row, tile)
         const int64_t H = e.H;
         float wsg[FN / 2], wsu[FN / 2];
-        int64_t jc[FN / 2];
-        bool jok[FN / 2];
 #pragma unroll
         for (int fn = 0; fn < FN / 2; ++fn) {
-            jc[fn] = (int64_t)nt * (BN / 2) + wn * (TN / 2) + fn * 32 + (lane & 31);
-            jok[fn] = jc[fn] < H;
-            wsg[fn] = jok[fn] ? e.w_scale[(int64_t)g * N + jc[fn]] : 0.0f;
-            wsu[fn] = jok[fn] ? e.w_scale[(int64_t)g * N + H + jc[fn]] : 0.0f;
+            const int64_t jc = (int64_t)nt * (BN / 2) + wn * (TN / 2) + fn * 32 + (lane & 31);
+            const bool ok = jc < H;
+            wsg[fn] = ok ? e.w_scale[(int64_t)g * N + jc] : 0.0f;
+            wsu[fn] = ok ? e.w_scale[(int64_t)g * N + H + jc] : 0.0f;
         }
+        epi_barrier();
+        CB_LDS uint8_t* st = (CB_LDS uint8_t*)smem;
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm) {
             if (!fvalid[fm]) continue;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int row = m0 + (WM * fm + wm) * 32 + (r >> 2) * 8 + lr + (r & 3);
-                const bool rowok = row < r1;
-                const float xs = rowok ? e.x_scale[row] : 0.0f;
-                float m = 0.0f;
+                const int lrow = (WM * fm + wm) * 32 + (r >> 2) * 8 + lr + (r & 3);
+                const int row = m0 + lrow < r1 ? m0 + lrow : r1 - 1;
+                const float xs = e.x_scale[row];
 #pragma unroll
                 for (int fn = 0; fn < FN / 2; ++fn) {
-                    if (rowok && jok[fn]) {
-                        const float v = swiglu((float)acc[fm][fn][r], (float)acc[fm][fn + FN / 2][r], xs,
-                                               wsg[fn], wsu[fn]);
-                        e.act[(int64_t)row * H + jc[fn]] = v;
-                        m = fmaxf(m, fabsf(v));
-                    }
+                    const float v = swiglu((float)acc[fm][fn][r], (float)acc[fm][fn + FN / 2][r], xs, wsg[fn], wsu[fn]);
+                    const int lcol = wn * (TN / 2) + fn * 32 + (lane & 31);
+                    *(CB_LDS float*)(st + lrow * C::EPI_PITCH + lcol * 4) = v;
                 }
-#pragma unroll
-                for (int o = 1; o < 32; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-                if ((lane & 31) == 0 && rowok) atomicMax(e.amax + row, __float_as_uint(m));
             }
         }
+        epi_barrier();
+        // two threads per row, 64 act columns (16 x float4) each
+        constexpr int TPR = C::NT / BM;           // threads per row
+        constexpr int CPT = (BN / 2) / TPR;       // act columns per thread
+        const int lrow = tid / TPR, part = tid % TPR;
+        const int row = m0 + lrow;
+        const int64_t j0 = (int64_t)nt * (BN / 2) + part * CPT;
+        float m = 0.0f;
+        if (row < r1) {
+            const CB_LDS v4f* src = (const CB_LDS v4f*)(st + lrow * C::EPI_PITCH + part * CPT * 4);
+            v4f* dst = reinterpret_cast<v4f*>(e.act + (int64_t)row * H + j0);
+#pragma unroll
+            for (int i = 0; i < CPT / 4; ++i) {
+                if (j0 + 4 * i < H) {
+                    const v4f v = src[i];
+                    dst[i] = v;
+                    m = fmaxf(m, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+                }
+            }
+        }
+#pragma unroll
+        for (int o = 1; o < TPR; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if (part == 0 && row < r1) atomicMax(e.amax + row, __float_as_uint(m));
     } else if constexpr (EPI == EPI_I32) {
         int32_t* ob = (int32_t*)e.out + b * e.out_bstride;
 #pragma unroll
@@ -296,32 +375,44 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
             }
         }
     } else {
+        // bf16 / fp16 tile [256][256] staged in LDS, then written with 16-byte stores
         ColDeq cd[FN];
-        int64_t cc[FN];
-        bool cok[FN];
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn) {
-            cc[fn] = (int64_t)nt * BN + wn * TN + fn * 32 + (lane & 31);
-            cok[fn] = cc[fn] < N;
-            cd[fn] = col_deq(e, g, b, cok[fn] ? cc[fn] : 0);
+            const int64_t cc = (int64_t)nt * BN + wn * TN + fn * 32 + (lane & 31);
+            cd[fn] = col_deq(e, g, b, cc < N ? cc : 0);
         }
-        uint16_t* ob = (uint16_t*)e.out + b * e.out_bstride;
+        epi_barrier();
+        CB_LDS uint8_t* st = (CB_LDS uint8_t*)smem;
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm) {
             if (!fvalid[fm]) continue;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int row = m0 + (WM * fm + wm) * 32 + (r >> 2) * 8 + lr + (r & 3);
-                if (row >= r1) continue;
+                const int lrow = (WM * fm + wm) * 32 + (r >> 2) * 8 + lr + (r & 3);
+                const int row = m0 + lrow < r1 ? m0 + lrow : r1 - 1;
                 const float pt = e.has_pt ? e.pertoken[row % e.pt_mod] : 1.0f;
 #pragma unroll
                 for (int fn = 0; fn < FN; ++fn) {
-                    if (cok[fn]) {
-                        const float v = apply_deq(e, cd[fn], acc[fm][fn][r], pt);
-                        ob[(int64_t)row * N + cc[fn]] = e.out_bf16 ? f32_to_bf16(v) : f32_to_f16(v);
-                    }
+                    const float v = apply_deq(e, cd[fn], acc[fm][fn][r], pt);
+                    const uint16_t h = e.out_bf16 ? f32_to_bf16_hw(v) : f32_to_f16(v);
+                    const int lcol = wn * TN + fn * 32 + (lane & 31);
+                    *(CB_LDS uint16_t*)(st + lrow * C::EPI_PITCH + lcol * 2) = h;
                 }
             }
+        }
+        epi_barrier();
+        uint16_t* ob = (uint16_t*)e.out + b * e.out_bstride;
+        constexpr int CHUNKS = BM * (BN * 2 / 16);  // 16-byte chunks in the tile
+#pragma unroll
+        for (int i = 0; i < CHUNKS / C::NT; ++i) {
+            const int id = tid + i * C::NT;
+            const int lrow = id / (BN * 2 / 16), ch = id % (BN * 2 / 16);
+            const int row = m0 + lrow;
+            const int64_t col = (int64_t)nt * BN + ch * 8;
+            if (row < r1 && col < N)
+                *reinterpret_cast<v4i*>(ob + (int64_t)row * N + col) =
+                    *(const CB_LDS v4i*)(st + lrow * C::EPI_PITCH + ch * 16);
         }
     }
 }

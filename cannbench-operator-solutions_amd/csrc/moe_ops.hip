@@ -78,7 +78,7 @@ static constexpr bool kSkinnyPrefetch = CB_SKINNY_PREFETCH;
 #define CB_LDS_CORE 1
 #endif
 #ifndef CB_LDS_WM
-#define CB_LDS_WM 2
+#define CB_LDS_WM 4
 #endif
 #ifndef CB_LDS_WN
 #define CB_LDS_WN 2
