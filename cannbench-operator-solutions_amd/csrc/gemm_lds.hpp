@@ -35,15 +35,27 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t lds_addr)
 {
-    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc),
+#ifndef CB_DMA_MOD
+#define CB_DMA_MOD ""
+#endif
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen" CB_DMA_MOD " lds" ::"v"(voff), "s"(rsrc),
                  "s"(lds_addr)
                  : "memory", "m0");
 }
 #pragma clang diagnostic pop
 
-// Workgroup barrier after the main loop: every wave's LDS reads are drained, so the stage buffers
-// can be reused for the epilogue staging.
-__device__ __forceinline__ void epi_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// Workgroup barrier after the main loop: every wave's LDS reads and DMAs (including the stages
+// issued past the end of K) are drained, so the stage buffers can be reused for epilogue staging.
+__device__ __forceinline__ void epi_barrier() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+#ifdef CB_PROFILE
+__device__ unsigned long long cb_prof[8];
+#define CB_PROF_T(v) uint64_t v = __builtin_amdgcn_s_memtime()
+#define CB_PROF_ADD(slot, t0) do { uint64_t _t = __builtin_amdgcn_s_memtime(); prof_acc[slot] += _t - (t0); } while (0)
+#else
+#define CB_PROF_T(v)
+#define CB_PROF_ADD(slot, t0)
+#endif
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt_barrier()
@@ -51,9 +63,12 @@ __device__ __forceinline__ void wait_vmcnt_barrier()
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-template <int WM, int WN, int STAGES>
+template <int WM, int WN, int STAGES, int BK_ = 64>
 struct LdsCfg {
-    static constexpr int BM = 256, BN = 256, BK = 64;
+    static constexpr int BM = 256, BN = 256, BK = BK_;
+    static constexpr int KS = BK / 32;    // 32-deep MFMA steps per stage
+    static constexpr int ACH = BK / 16;   // 16-byte chunks per A row
+    static_assert(BK == 64 || BK == 128, "stage depth");
     static constexpr int NW = WM * WN, NT = 64 * NW;
     static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
     static constexpr int A_BYTES = BM * BK, B_BYTES = BK * BN, STAGE = A_BYTES + B_BYTES;
@@ -69,10 +84,14 @@ struct LdsCfg {
     static_assert(FN >= 2 && FN % 2 == 0, "wave tile must hold gate/up pairs");
 };
 
-template <int EPI, int WM, int WN, int STAGES>
+template <int EPI, int WM, int WN, int STAGES, int BKT>
 __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArgs a)
 {
-    using C = LdsCfg<WM, WN, STAGES>;
+    using C = LdsCfg<WM, WN, STAGES, BKT>;
+    constexpr int KS = C::KS, ACH = C::ACH;
+    // A swizzle key: spreads the 16 rows of a ds_read_b128 phase over all 64 banks
+    // (BK 64: 4 rows per 256 bytes, key (r >> 2) & 3; BK 128: 2 rows per 256 bytes, key (r >> 1) & 7)
+    auto a_swz = [](int r) { return ACH == 4 ? ((r >> 2) & 3) : ((r >> 1) & 7); };
     constexpr int BM = C::BM, BN = C::BN, BK = C::BK, NW = C::NW, TN = C::TN, FM = C::FM,
                   FN = C::FN;
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
@@ -86,7 +105,10 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
 
     // ---- tile selection (XCD remap + GROUP_M swizzle) -------------------------------------
     const int pid = xcd_remap(blockIdx.x, gridDim.x);
-    constexpr int GROUP_M = 4;
+#ifndef CB_GROUP_M
+#define CB_GROUP_M 4
+#endif
+    constexpr int GROUP_M = CB_GROUP_M;
     const int T_m = a.gt.total_mtiles, T_n = a.ntiles;
     const int per_group = GROUP_M * T_n;
     const int gid = pid / per_group;
@@ -112,8 +134,8 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
 #pragma unroll
     for (int i = 0; i < C::A_ISSUE; ++i) {
         const int cid = (i * NW + wave) * 64 + lane;  // 16-byte chunk id in the A tile
-        const int row = cid >> 2, pos = cid & 3;
-        const int q = pos ^ ((row >> 2) & 3);
+        const int row = cid / ACH, pos = cid % ACH;
+        const int q = pos ^ a_swz(row);
         const int rr = row < vrows ? row : vrows - 1;
         a_off[i] = (uint32_t)rr * (uint32_t)K + (uint32_t)(q * 16);
     }
@@ -161,25 +183,25 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
     // A: fragment fm of wave row wm covers tile rows 32 (WM fm + wm) .. +32 (row blocks are
     // interleaved over the WM waves so a partial tile loads them evenly); lane % 32 picks the row,
     // k-chunk q = 2 ks + lane / 32
-    uint32_t a_rd[FM][2];
+    uint32_t a_rd[FM][KS];
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
         const int r = (WM * fm + wm) * 32 + (lane & 31);
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        for (int ks = 0; ks < KS; ++ks) {
             const int q = 2 * ks + (lane >> 5);
-            a_rd[fm][ks] = (uint32_t)(r * BK + ((q ^ ((r >> 2) & 3)) << 4));
+            a_rd[fm][ks] = (uint32_t)(r * BK + ((q ^ a_swz(r)) << 4));
         }
     }
     // B: group gq = lane / 16 -> k half (gq >> 1), column half (gq & 1); in-group lane s -> row
     // offset s >> 1, byte half s & 1
     const int gq = lane >> 4, s = lane & 15;
-    uint32_t b_rd[FN][2][2];  // [fn][ks][low/high 8 k]
+    uint32_t b_rd[FN][KS][2];  // [fn][ks][low/high 8 k]
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) {
         const int cc = (tcol(fn) >> 4) + (gq & 1);
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+        for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf) {
                 const int row = ks * 32 + (gq >> 1) * 16 + hf * 8 + (s >> 1);
@@ -203,31 +225,24 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
             for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0;
 
     const int nk = (int)((K + BK - 1) / BK);
-    // Prologue: every LDS buffer gets a stage in flight.
+    // Prologue: every LDS buffer gets a stage in flight.  The loop below issues one stage per
+    // iteration unconditionally, so the number of DMAs in flight is always the same and every
+    // wait is a compile-time constant; stages past the end of K only fetch zeros or unused bytes
+    // into buffers that are never read again.
 #pragma unroll
-    for (int st = 0; st < STAGES; ++st)
-        if (st < nk) issue_stage(st);
-
-    // Wait until stage `kt` is in LDS for every wave: own DMAs of stages after kt may stay in
-    // flight (`later` of them), own LDS reads are drained (the buffer about to be refilled was
-    // read by them), then the workgroup barrier.
-    auto wait_stage = [&](int later) {
-        static_assert(STAGES >= 2 && STAGES <= 5, "wait chain below covers up to 4 later stages");
-        if (STAGES >= 5 && later >= 4) wait_vmcnt_barrier<4 * C::ISSUE>();
-        else if (STAGES >= 4 && later >= 3) wait_vmcnt_barrier<3 * C::ISSUE>();
-        else if (STAGES >= 4 && later >= 2) wait_vmcnt_barrier<2 * C::ISSUE>();
-        else if (STAGES >= 3 && later >= 1) wait_vmcnt_barrier<C::ISSUE>();
-        else wait_vmcnt_barrier<0>();
-    };
+    for (int st = 0; st < STAGES; ++st) issue_stage(st);
 
     // Software pipeline per stage kt (fragments of half-stage ks = 0 already in registers):
-    //   read ks = 1 fragments | MFMAs on ks = 0 | barrier for stage kt + 1, refill buffer of kt,
-    //   read kt + 1 ks = 0 fragments | MFMAs on ks = 1
-    // so LDS read latency hides behind MFMAs and the barrier sits between two MFMA groups.
+    //   read ks = 1 fragments | MFMAs on ks = 0 | barrier for stage kt + 1, refill the buffer
+    //   of stage kt, read kt + 1 ks = 0 fragments | MFMAs on ks = 1
+    // Within each half the reads are interleaved one-for-one with the MFMAs (sched_group_barrier),
+    // which keeps at most one fragment set of LDS reads outstanding: the in-order lgkmcnt counter
+    // (4 bits) then lets each MFMA wait only for the set it consumes.
     auto kloop = [&](auto nv_const) {
         constexpr int NV = decltype(nv_const)::value;  // fragments that get MFMAs
-        v4i a0[NV > 0 ? NV : 1], b0[FN], a1[NV > 0 ? NV : 1], b1[FN];
-        auto load = [&](int kt, int ks, v4i (&af)[NV > 0 ? NV : 1], v4i (&bf)[FN]) {
+        constexpr int NVA = NV > 0 ? NV : 1;
+        v4i a0[NVA], b0[FN], a1[NVA], b1[FN];
+        auto load = [&](int kt, int ks, v4i (&af)[NVA], v4i (&bf)[FN]) {
             if constexpr (NV > 0) {
                 const CB_LDS uint8_t* base = (const CB_LDS uint8_t*)smem + (kt % STAGES) * C::STAGE;
 #ifndef CB_ABLATE_NO_LDSREAD
@@ -247,7 +262,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
 #endif
             }
         };
-        auto mma = [&](const v4i (&af)[NV > 0 ? NV : 1], const v4i (&bf)[FN]) {
+        auto mma = [&](const v4i (&af)[NVA], const v4i (&bf)[FN]) {
             if constexpr (NV > 0) {
 #ifndef CB_ABLATE_NO_MFMA
 #pragma unroll
@@ -263,21 +278,63 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
 #endif
             }
         };
-        wait_stage(nk - 1 < STAGES - 1 ? nk - 1 : STAGES - 1);
+        // one DS read after each MFMA while reads remain, then the remaining MFMAs
+        auto interleave = [&]() {
+#if !defined(CB_NO_SCHED_HINTS) && !defined(CB_ABLATE_NO_MFMA) && !defined(CB_ABLATE_NO_LDSREAD)
+            if constexpr (NV > 0) {
+                constexpr int NMFMA = NV * FN, NREAD = NV + 2 * FN;
+                constexpr int PAIRS = NMFMA < NREAD ? NMFMA : NREAD;
+#pragma unroll
+                for (int i = 0; i < PAIRS; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);  // 1 MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);  // 1 DS read
+                }
+                if constexpr (NMFMA > PAIRS) __builtin_amdgcn_sched_group_barrier(0x0008, NMFMA - PAIRS, 0);
+                if constexpr (NREAD > PAIRS) __builtin_amdgcn_sched_group_barrier(0x0100, NREAD - PAIRS, 0);
+            }
+#endif
+        };
+        constexpr int LATER = STAGES - 2;  // stages after the awaited one that stay in flight
+#ifdef CB_PROFILE
+        uint64_t prof_acc[4] = {0, 0, 0, 0};
+        CB_PROF_T(tstart);
+#endif
+        wait_vmcnt_barrier<(STAGES - 1) * C::ISSUE>();
         load(0, 0, a0, b0);
         for (int kt = 0; kt < nk; ++kt) {
-            load(kt, 1, a1, b1);
-            mma(a0, b0);
-            if (kt + 1 < nk) {
-                const int later = nk - kt - 2 < STAGES - 2 ? nk - kt - 2 : STAGES - 2;
-                wait_stage(later);
+#pragma unroll
+            for (int ks = 0; ks < KS; ks += 2) {
+                // step ks (in a0/b0) with step ks + 1 loading, then step ks + 1 with the next
+                // stage's first step (or ks + 2) loading
+                load(kt, ks + 1, a1, b1);
+                mma(a0, b0);
+                interleave();
+                if (ks + 2 == KS) {
+                    CB_PROF_T(tw);
+                    wait_vmcnt_barrier<LATER * C::ISSUE>();
+                    CB_PROF_ADD(0, tw);
+                    CB_PROF_T(td);
 #ifndef CB_ABLATE_NO_DMA
-                if (kt + STAGES < nk) issue_stage(kt + STAGES);
+                    issue_stage(kt + STAGES);
 #endif
-                load(kt + 1, 0, a0, b0);
+                    CB_PROF_ADD(1, td);
+                    load(kt + 1, 0, a0, b0);
+                } else {
+                    load(kt, ks + 2, a0, b0);
+                }
+                mma(a1, b1);
+                interleave();
             }
-            mma(a1, b1);
         }
+#ifdef CB_PROFILE
+        CB_PROF_ADD(2, tstart);
+        if (lane == 0) {
+            atomicAdd(&cb_prof[0], prof_acc[0]);
+            atomicAdd(&cb_prof[1], prof_acc[1]);
+            atomicAdd(&cb_prof[2], prof_acc[2]);
+            atomicAdd(&cb_prof[3], 1ull);
+        }
+#endif
     };
     static_assert(FM <= 4, "loop variants below cover up to 4 fragments");
     if (nvf >= FM) kloop(std::integral_constant<int, FM>());

@@ -71,7 +71,7 @@ static GmsqWorkspace gmsq_workspace(int64_t M, int64_t N)
 static constexpr int kSkinnyMaxRows = 32;  // groups up to this many rows take the skinny core
 static constexpr int kTiledBM = 128;
 #ifndef CB_SKINNY_PREFETCH
-#define CB_SKINNY_PREFETCH 1
+#define CB_SKINNY_PREFETCH 0
 #endif
 static constexpr bool kSkinnyPrefetch = CB_SKINNY_PREFETCH;
 #ifndef CB_LDS_CORE
@@ -86,8 +86,11 @@ static constexpr bool kSkinnyPrefetch = CB_SKINNY_PREFETCH;
 #ifndef CB_LDS_STAGES
 #define CB_LDS_STAGES 4
 #endif
+#ifndef CB_LDS_BK
+#define CB_LDS_BK 64
+#endif
 static constexpr bool kUseLdsCore = CB_LDS_CORE;
-static constexpr int kLdsWM = CB_LDS_WM, kLdsWN = CB_LDS_WN, kLdsStages = CB_LDS_STAGES;
+static constexpr int kLdsWM = CB_LDS_WM, kLdsWN = CB_LDS_WN, kLdsStages = CB_LDS_STAGES, kLdsBK = CB_LDS_BK;
 
 // Optional per-thread instrumentation: events recorded around the next main GEMM kernel launch
 // (set by cb_set_kernel_timing, consumed and cleared by that launch).
@@ -135,10 +138,10 @@ static void launch_gemm(GemmArgs& a, const int64_t* gl, int64_t E, int64_t batch
     }
     a.ntiles = (int)((EPI == EPI_SWIGLU) ? (Ncols + 127) / 128 : (Ncols + 255) / 256);
     if (kUseLdsCore) {
-        using Cfg = LdsCfg<kLdsWM, kLdsWN, kLdsStages>;
+        using Cfg = LdsCfg<kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
         build_group_table(a.gt, gl, E, Cfg::BM);
         const int64_t blocks = (int64_t)a.gt.total_mtiles * a.ntiles;
-        auto kern = lds_gemm_kernel<EPI, kLdsWM, kLdsWN, kLdsStages>;
+        auto kern = lds_gemm_kernel<EPI, kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
         static bool attr_set = false;  // per template instance; idempotent, so a benign race
         if (!attr_set) {
             (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS_BYTES);
@@ -373,3 +376,15 @@ extern "C" int cb_grouped_matmul_int32(const int8_t* x, const int8_t* weight, co
     launch_gemm<EPI_I32>(a, group_list, E, 1, fast, (hipStream_t)stream);
     return check_launch();
 }
+
+#ifdef CB_PROFILE
+extern "C" void cb_debug_profile(unsigned long long* out, int reset)
+{
+    (void)hipDeviceSynchronize();
+    (void)hipMemcpyFromSymbol(out, HIP_SYMBOL(cb_prof), sizeof(unsigned long long) * 8);
+    if (reset) {
+        unsigned long long z[8] = {0};
+        (void)hipMemcpyToSymbol(HIP_SYMBOL(cb_prof), z, sizeof(z));
+    }
+}
+#endif
