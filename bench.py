@@ -155,6 +155,28 @@ def bench_qmm(steps, warmup, dev):
             "config": {"workload": "qmm", "M": M, "K": K, "N": N}}
 
 
+def bench_copy(steps, warmup, dev):
+    """Plain device copy of 2 GiB: the calibration kernel for the FETCH_SIZE / WRITE_SIZE counters."""
+    n = 2 << 30
+    a = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    ms = time_op(lambda: b.copy_(a), steps, warmup)
+    return {"ms": ms, "gbs": 2 * n / (ms * 1e-3) / 1e9, "bytes_read": n, "bytes_written": n}
+
+
+def traffic_from_profiles(kernel_tag):
+    """HBM bytes per launch of a kernel as recorded in profiles/<kernel_tag>_traffic.md (a line
+    'traffic_bytes_per_launch: N', derived from FETCH_SIZE + WRITE_SIZE scaled by the copy-kernel
+    calibration), or None when no such summary is committed."""
+    path = os.path.join(ROOT, "profiles", f"{kernel_tag}_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.strip().startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1].strip()))
+    return None
+
+
 def cpu_baseline(d, budget_s=12.0):
     """The C oracle on the host cores over whole experts of the prefill config, until ~budget_s."""
     from oracle import oracle as orc
@@ -191,7 +213,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", default="prefill,decode,ardq,qmm")
+    ap.add_argument("--only", default="prefill,decode,ardq,qmm",
+                    help="comma list of prefill, decode, ardq, qmm, copy")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -231,6 +254,14 @@ def main():
         q = bench_qmm(args.steps, args.warmup, dev)
         out["qmm"] = {"value": round(q["tops"], 2), "unit": "TOPS", "ms_per_step": round(q["ms"], 4),
                       "roofline": q["roofline"], "config": q["config"]}
+    if "copy" in only:
+        c = bench_copy(args.steps, args.warmup, dev)
+        out["copy"] = {"value": round(c["gbs"], 1), "unit": "GB/s", "ms_per_step": round(c["ms"], 4),
+                       "bytes_read": c["bytes_read"], "bytes_written": c["bytes_written"]}
+    if out.get("roofline") is not None:
+        out["roofline"]["traffic"] = traffic_from_profiles("prefill_gemm")
+    if "decode" in out:
+        out["decode"]["roofline"]["traffic"] = traffic_from_profiles("decode_gemm")
     if not args.no_cpu and "prefill" in keep:
         out["cpu_baseline"] = cpu_baseline(keep["prefill"])
     print(json.dumps(out), flush=True)

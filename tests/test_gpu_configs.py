@@ -1,0 +1,129 @@
+"""GPU parity at the benchmark configurations' full sizes.
+
+Whole-tensor oracle comparisons where the CPU oracle finishes in seconds (DynamicQuant,
+AddRmsNormDynamicQuant, QuantMatmul), sampled experts / rows for the MoE configurations (the
+oracle is checked on whole experts, including every partial 256-row tile of them), and
+size-independent properties on every row: |y| <= 127, the row maximum lands on 126/127, scales are
+finite and positive, the int32 core is bit-exact.
+"""
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+cfgs = importlib.import_module("cannbench-operator-solutions_amd.configs")
+
+
+def bits16(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def int8_close(got, ref, max_frac=0.01):
+    d = np.abs(got.astype(np.int32) - ref.astype(np.int32))
+    assert d.max() <= 1, f"int8 diff {d.max()}"
+    assert (d > 0).mean() <= max_frac, f"{(d > 0).mean():.4%} differ by 1 LSB"
+
+
+@pytest.fixture(scope="module")
+def prefill():
+    d = cfgs.make_gmsq_prefill("cuda")
+    yield d
+    del d
+    torch.cuda.empty_cache()
+
+
+def _sample_experts(gl, n, seed=0):
+    starts = [0] + gl[:-1]
+    rows = np.array([e - s for s, e in zip(starts, gl)])
+    nz = np.nonzero(rows)[0]
+    rng = np.random.default_rng(seed)
+    pick = set(rng.choice(nz, size=min(n, len(nz)), replace=False).tolist())
+    pick.add(int(nz[np.argmin(rows[nz])]))   # lightest non-empty expert
+    return sorted(pick), starts
+
+
+def test_dynamic_quant_config1(cb, orc):
+    d = cfgs.make_dq("cuda")
+    y, s = cb.dynamic_quant(d["x"])
+    yr, sr = orc.dynamic_quant(bits16(d["x"]), "f16")
+    np.testing.assert_allclose(s.cpu().numpy(), sr, rtol=1e-6)
+    int8_close(y.cpu().numpy(), yr)
+
+
+def test_ardq_config2(cb, orc):
+    d = cfgs.make_ardq("cuda")
+    y, xo, s = cb.add_rms_norm_dynamic_quant(d["x1"], d["x2"], d["gamma"], d["epsilon"])
+    yr, xor_, sr = orc.ardq(bits16(d["x1"]), bits16(d["x2"]), bits16(d["gamma"]), "bf16", d["epsilon"])
+    np.testing.assert_array_equal(bits16(xo), xor_)
+    np.testing.assert_allclose(s.cpu().numpy(), sr, rtol=1e-5)
+    int8_close(y.cpu().numpy(), yr)
+
+
+def test_quant_matmul_config3(cb, orc):
+    d = cfgs.make_qmm("cuda")
+    out = cb.quant_matmul(d["x1"], d["x2"], d["scale"], pertoken_scale=d["pertoken_scale"], output_dtype="bfloat16")
+    ref = orc.quant_matmul(d["x1"].cpu().numpy(), d["x2"].cpu().numpy(), d["scale"].cpu().numpy(),
+                           pertoken=d["pertoken_scale"].cpu().numpy(), out_dtype="bf16")
+    np.testing.assert_array_equal(bits16(out), ref)
+
+
+def test_gmsq_prefill_int32_core_exact(cb, orc, prefill):
+    """The int32 grouped GEMM at the prefill shape, bit-exact on whole sampled experts."""
+    d = prefill
+    c = cb.grouped_matmul_int32(d["x"], d["weight"], d["group_list"])
+    experts, starts = _sample_experts(d["group_list"], 3, seed=1)
+    for g in experts:
+        s, e = starts[g], d["group_list"][g]
+        s_rows = slice(s, min(e, s + 600))  # up to 600 rows: full tiles plus a partial one
+        ref = orc.i8_gemm(d["x"][s_rows].cpu().numpy(), d["weight"][g].cpu().numpy())
+        np.testing.assert_array_equal(c[s_rows].cpu().numpy(), ref, err_msg=f"expert {g}")
+    del c
+
+
+def test_gmsq_prefill_config4(cb, orc, prefill):
+    d = prefill
+    y, ys = cb.grouped_matmul_swiglu_quant(d["x"], d["weight"], d["weight_scale"], d["x_scale"], d["group_list"])
+    torch.cuda.synchronize()
+    yn = y.cpu().numpy()
+    ysn = ys.cpu().numpy()
+    # every row: |y| <= 127 by construction of int8, row max on 126 / 127, finite positive scales
+    rmax = np.abs(yn.astype(np.int32)).max(axis=1)
+    assert np.isin(rmax, [126, 127]).all()
+    assert np.isfinite(ysn).all() and (ysn > 0).all()
+    # whole sampled experts against the oracle (heavy, mid and the lightest expert)
+    experts, starts = _sample_experts(d["group_list"], 6, seed=2)
+    ws = d["weight_scale"].cpu().numpy()
+    xs = d["x_scale"].cpu().numpy()
+    for g in experts:
+        s, e = starts[g], d["group_list"][g]
+        e2 = min(e, s + 700)
+        yr, ysr = orc.gmsq(d["x"][s:e2].cpu().numpy(), d["weight"][g:g + 1].cpu().numpy(), ws[g:g + 1],
+                           xs[s:e2], np.array([e2 - s]))
+        np.testing.assert_allclose(ysn[s:e2], ysr, rtol=1e-5, err_msg=f"expert {g}")
+        int8_close(yn[s:e2], yr)
+
+
+def test_gmsq_decode_and_down_config5(cb, orc):
+    d = cfgs.make_gmsq_decode("cuda")
+    y, ys = cb.grouped_matmul_swiglu_quant(d["x"], d["weight"], d["weight_scale"], d["x_scale"], d["group_list"])
+    out = cb.grouped_matmul_quant(y, d["down_weight"], d["down_weight_scale"], ys, d["group_list"])
+    torch.cuda.synchronize()
+    yn, ysn, outn = y.cpu().numpy(), ys.cpu().numpy(), bits16(out)
+    assert np.isin(np.abs(yn.astype(np.int32)).max(axis=1), [126, 127]).all()
+    experts, starts = _sample_experts(d["group_list"], 24, seed=3)
+    ws = d["weight_scale"].cpu().numpy()
+    xs = d["x_scale"].cpu().numpy()
+    ws2 = d["down_weight_scale"].cpu().numpy()
+    for g in experts:
+        s, e = starts[g], d["group_list"][g]
+        yr, ysr = orc.gmsq(d["x"][s:e].cpu().numpy(), d["weight"][g:g + 1].cpu().numpy(), ws[g:g + 1],
+                           xs[s:e], np.array([e - s]))
+        np.testing.assert_allclose(ysn[s:e], ysr, rtol=1e-5)
+        int8_close(yn[s:e], yr, max_frac=0.02)
+        # down-projection on the GPU's own GMSQ output: bit-exact
+        outr = orc.grouped_matmul_quant(yn[s:e], d["down_weight"][g:g + 1].cpu().numpy(), ws2[g:g + 1],
+                                        ysn[s:e], np.array([e - s]))
+        np.testing.assert_array_equal(outn[s:e], outr, err_msg=f"expert {g}")
