@@ -173,6 +173,24 @@ __global__ __launch_bounds__(512) void dq_kernel(const uint16_t* __restrict__ x,
     }
 }
 
+// DynamicQuant for rows longer than one workgroup's register slice: two passes over the row
+// (abs-max, then quantise), the second one served mostly from L2.
+template <bool BF16>
+__global__ __launch_bounds__(512) void dq_long_kernel(const uint16_t* __restrict__ x, int64_t n,
+                                                      int8_t* __restrict__ y, float* __restrict__ scale)
+{
+    __shared__ float red[2 * kRowMaxWaves];
+    const uint16_t* xr = x + (int64_t)blockIdx.x * n;
+    int8_t* yr = y + (int64_t)blockIdx.x * n;
+    float s = 0.0f, a = 0.0f;
+    for (int64_t j = threadIdx.x; j < n; j += blockDim.x) a = fmaxf(a, fabsf(ld16<BF16>(xr[j])));
+    block_sum_max(s, a, red);
+    a = fmaxf(a, 1e-12f);
+    if (threadIdx.x == 0) scale[blockIdx.x] = a * kInv127;
+    const float inv = 127.0f * (1.0f / a);
+    for (int64_t j = threadIdx.x; j < n; j += blockDim.x) yr[j] = (int8_t)rint16(ld16<BF16>(xr[j]) * inv);
+}
+
 // ---------------------------------------------------------------------------------------------
 // Host side: pick (VEC, threads, NV) and launch.
 // ---------------------------------------------------------------------------------------------
@@ -302,10 +320,17 @@ extern "C" int cb_dynamic_quant(const void* x, int dtype, int64_t rows, int64_t 
     if (rows < 0 || row_len < 0) return CB_ERR_SHAPE;
     if (row_len == 0) return CB_ERR_EMPTY;  // the reference requires a non-zero last dimension
     if (rows == 0) return CB_OK;
-    if (row_len > 16384 || rows > 0x7fffffffLL) return CB_ERR_SHAPE;
+    if (rows > 0x7fffffffLL) return CB_ERR_SHAPE;
     if (!x || !y || !scale) return CB_ERR_NULL_POINTER;
-    RowPlan p = plan_row(row_len, aligned(x, 16) && aligned(y, 8));
     hipStream_t st = (hipStream_t)stream;
+    if (row_len > 16384) {  // longer than a register-resident row slice
+        if (dtype == CB_DT_BFLOAT16)
+            hipLaunchKernelGGL(dq_long_kernel<true>, dim3((unsigned)rows), dim3(512), 0, st, (const uint16_t*)x, row_len, y, scale);
+        else
+            hipLaunchKernelGGL(dq_long_kernel<false>, dim3((unsigned)rows), dim3(512), 0, st, (const uint16_t*)x, row_len, y, scale);
+        return hipGetLastError() == hipSuccess ? CB_OK : CB_ERR_LAUNCH;
+    }
+    RowPlan p = plan_row(row_len, aligned(x, 16) && aligned(y, 8));
     auto xp = (const uint16_t*)x;
     hipError_t e;
     if (dtype == CB_DT_BFLOAT16)

@@ -77,7 +77,7 @@ def test_ardq_3d_input(cb, orc):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("rows,n", [(1024, 4096), (7, 1000), (3, 12288)])
+@pytest.mark.parametrize("rows,n", [(1024, 4096), (7, 1000), (3, 12288), (2, 20000)])
 def test_dynamic_quant(cb, orc, dtype, rows, n):
     g = cpu_gen(rows + n)
     x = torch.randn(rows, n, generator=g)
