@@ -104,7 +104,13 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
     const int64_t b = blockIdx.y;
 
     // ---- tile selection (XCD remap + GROUP_M swizzle) -------------------------------------
+    // Measured on the prefill and dense shapes: the plain dispatch order (workgroups round-robin
+    // over the XCDs) is as good as or better than an XCD-contiguous remap of the tile order.
+#ifdef CB_XCD_REMAP
     const int pid = xcd_remap(blockIdx.x, gridDim.x);
+#else
+    const int pid = blockIdx.x;
+#endif
 #ifndef CB_GROUP_M
 #define CB_GROUP_M 4
 #endif

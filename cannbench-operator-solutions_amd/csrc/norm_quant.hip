@@ -9,6 +9,8 @@
 //   ARDQ  operators/addrmsnormdynamicquant/csrc/ops/add_rms_norm_dynamic_quant/op_kernel/
 //         add_rms_norm_dynamic_quant_kernel.cpp:15-30 (algebra), 440-503 (per-row order of operations)
 //   DQ    operators/dynamicquant/csrc/ops/dynamic_quant/op_kernel/dynamic_quant_kernel.cpp:15-26,240-282
+#include <climits>
+
 #include "common.hpp"
 #include "host_util.hpp"
 
@@ -41,12 +43,19 @@ struct Vec16 {
     uint16_t v[VEC];
 };
 
+#ifndef CB_ROW_NT
+#define CB_ROW_NT 1
+#endif
+typedef int rv4i __attribute__((ext_vector_type(4)));
+
 template <int VEC>
 __device__ __forceinline__ Vec16<VEC> ldv(const uint16_t* p)
 {
     Vec16<VEC> r;
     if constexpr (VEC == 8) {
-        uint4 q = *reinterpret_cast<const uint4*>(p);
+        // row data is read exactly once: nontemporal loads keep it from displacing other lines
+        const rv4i q = CB_ROW_NT ? __builtin_nontemporal_load(reinterpret_cast<const rv4i*>(p))
+                                 : *reinterpret_cast<const rv4i*>(p);
         __builtin_memcpy(r.v, &q, 16);
     } else {
 #pragma unroll
@@ -59,9 +68,10 @@ template <int VEC>
 __device__ __forceinline__ void stv(uint16_t* p, const Vec16<VEC>& r)
 {
     if constexpr (VEC == 8) {
-        uint4 q;
+        rv4i q;
         __builtin_memcpy(&q, r.v, 16);
-        *reinterpret_cast<uint4*>(p) = q;
+        if (CB_ROW_NT) __builtin_nontemporal_store(q, reinterpret_cast<rv4i*>(p));
+        else *reinterpret_cast<rv4i*>(p) = q;
     } else {
 #pragma unroll
         for (int j = 0; j < VEC; ++j) p[j] = r.v[j];
@@ -72,10 +82,12 @@ template <int VEC>
 __device__ __forceinline__ void sty8(int8_t* p, const int* q)
 {
     if constexpr (VEC == 8) {
-        uint2 w;
-        w.x = pack4_i8(q[0], q[1], q[2], q[3]);
-        w.y = pack4_i8(q[4], q[5], q[6], q[7]);
-        *reinterpret_cast<uint2*>(p) = w;
+        typedef int rv2i __attribute__((ext_vector_type(2)));
+        rv2i w;
+        w[0] = (int)pack4_i8(q[0], q[1], q[2], q[3]);
+        w[1] = (int)pack4_i8(q[4], q[5], q[6], q[7]);
+        if (CB_ROW_NT) __builtin_nontemporal_store(w, reinterpret_cast<rv2i*>(p));
+        else *reinterpret_cast<rv2i*>(p) = w;
     } else {
 #pragma unroll
         for (int j = 0; j < VEC; ++j) p[j] = (int8_t)q[j];
@@ -200,17 +212,43 @@ struct RowPlan {
     int nv;
 };
 
+#ifndef CB_ROW_MAX_THREADS
+#define CB_ROW_MAX_THREADS 512
+#endif
+
+// Row split: VEC elements per access (8 when rows are 16-byte aligned), `threads` a multiple of 64,
+// NV accesses per thread.  Vector path: the (threads, NV <= 8) pair with the fewest idle slots,
+// preferring wider workgroups up to CB_ROW_MAX_THREADS.  Scalar path: powers of two.
 static RowPlan plan_row(int64_t n, bool aligned16)
 {
     RowPlan p;
     p.vec = (aligned16 && n % 8 == 0) ? 8 : 1;
     const int64_t nvec = n / p.vec;
+    if (p.vec == 8) {
+        int best_t = 64, best_nv = 8;
+        int64_t best_waste = INT64_MAX;
+        for (int t = 64; t <= 512; t += 64) {
+            const int64_t nv = (nvec + t - 1) / t;
+            if (nv > 8) continue;
+            const int64_t waste = t * nv - nvec;
+            const bool better = waste < best_waste ||
+                                (waste == best_waste && t <= CB_ROW_MAX_THREADS && (best_t > CB_ROW_MAX_THREADS || t > best_t));
+            if (better) {
+                best_waste = waste;
+                best_t = t;
+                best_nv = (int)nv;
+            }
+        }
+        p.threads = best_t;
+        p.nv = best_nv;
+        return p;
+    }
     int64_t t = (nvec + 63) / 64 * 64;
     p.threads = (int)(t < 64 ? 64 : (t > 256 ? 256 : t));
     int64_t need = (nvec + p.threads - 1) / p.threads;
     int nv = 1;
     while (nv < need) nv <<= 1;
-    if (p.vec == 1 && nv > 32) {  // keep the register slice bounded: widen the workgroup instead
+    if (nv > 32) {  // keep the register slice bounded: widen the workgroup instead
         p.threads = 512;
         need = (nvec + 511) / 512;
         nv = 1;
@@ -231,21 +269,28 @@ static hipError_t launch_ardq_v(const RowPlan& p, int64_t rows, const uint16_t* 
         hipLaunchKernelGGL((ardq_kernel<BF16, VEC, NVV>), grid, block, 0, st, x1, x2, g, n, eps,   \
                            invN, y, xo, sc);                                                       \
         break;
-    switch (p.nv) {
-        CB_ARDQ_CASE(1)
-        CB_ARDQ_CASE(2)
-        CB_ARDQ_CASE(4)
-        CB_ARDQ_CASE(8)
-        default:
-            if constexpr (VEC == 1) {
-                switch (p.nv) {
-                    CB_ARDQ_CASE(16)
-                    CB_ARDQ_CASE(32)
-                    default: return hipErrorInvalidValue;
-                }
-            } else {
-                return hipErrorInvalidValue;
-            }
+    if constexpr (VEC == 8) {
+        switch (p.nv) {
+            CB_ARDQ_CASE(1)
+            CB_ARDQ_CASE(2)
+            CB_ARDQ_CASE(3)
+            CB_ARDQ_CASE(4)
+            CB_ARDQ_CASE(5)
+            CB_ARDQ_CASE(6)
+            CB_ARDQ_CASE(7)
+            CB_ARDQ_CASE(8)
+            default: return hipErrorInvalidValue;
+        }
+    } else {
+        switch (p.nv) {
+            CB_ARDQ_CASE(1)
+            CB_ARDQ_CASE(2)
+            CB_ARDQ_CASE(4)
+            CB_ARDQ_CASE(8)
+            CB_ARDQ_CASE(16)
+            CB_ARDQ_CASE(32)
+            default: return hipErrorInvalidValue;
+        }
     }
 #undef CB_ARDQ_CASE
     return hipGetLastError();
@@ -260,21 +305,28 @@ static hipError_t launch_dq_v(const RowPlan& p, int64_t rows, const uint16_t* x,
     case NVV:                                                                                      \
         hipLaunchKernelGGL((dq_kernel<BF16, VEC, NVV>), grid, block, 0, st, x, n, y, sc);          \
         break;
-    switch (p.nv) {
-        CB_DQ_CASE(1)
-        CB_DQ_CASE(2)
-        CB_DQ_CASE(4)
-        CB_DQ_CASE(8)
-        default:
-            if constexpr (VEC == 1) {
-                switch (p.nv) {
-                    CB_DQ_CASE(16)
-                    CB_DQ_CASE(32)
-                    default: return hipErrorInvalidValue;
-                }
-            } else {
-                return hipErrorInvalidValue;
-            }
+    if constexpr (VEC == 8) {
+        switch (p.nv) {
+            CB_DQ_CASE(1)
+            CB_DQ_CASE(2)
+            CB_DQ_CASE(3)
+            CB_DQ_CASE(4)
+            CB_DQ_CASE(5)
+            CB_DQ_CASE(6)
+            CB_DQ_CASE(7)
+            CB_DQ_CASE(8)
+            default: return hipErrorInvalidValue;
+        }
+    } else {
+        switch (p.nv) {
+            CB_DQ_CASE(1)
+            CB_DQ_CASE(2)
+            CB_DQ_CASE(4)
+            CB_DQ_CASE(8)
+            CB_DQ_CASE(16)
+            CB_DQ_CASE(32)
+            default: return hipErrorInvalidValue;
+        }
     }
 #undef CB_DQ_CASE
     return hipGetLastError();
