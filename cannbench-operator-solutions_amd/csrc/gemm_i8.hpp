@@ -197,8 +197,11 @@ __device__ __forceinline__ void set_comp(uint4& v, int i, u32 x)
 //   group c = l % 16 (16 consecutive weight columns); after the in-register 16x16 byte transpose
 //   the lane holds 16 B operands, one per column, and MFMA j yields column (16 c + j).
 // ============================================================================================
+#ifndef CB_SKINNY_OCC
+#define CB_SKINNY_OCC 3
+#endif
 template <int EPI, bool PREFETCH>
-__global__ __launch_bounds__(256, PREFETCH ? 2 : 3) void skinny_kernel(const GemmArgs a)
+__global__ __launch_bounds__(256, PREFETCH ? 2 : CB_SKINNY_OCC) void skinny_kernel(const GemmArgs a)
 {
     __shared__ int red[3][4][16][64];  // partial sums handed to the wave that owns them (48 KiB)
 

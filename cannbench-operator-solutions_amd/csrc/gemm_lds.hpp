@@ -165,6 +165,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
     }
 
     const uint32_t lds_base = (uint32_t)(uintptr_t)(CB_LDS uint8_t*)smem;
+    const int nk = (int)((K + BK - 1) / BK);
     auto issue_stage = [&](int kt) {
         const uint32_t sa = lds_base + (uint32_t)((kt % STAGES) * C::STAGE);
         const uint32_t sb = sa + C::A_BYTES;
@@ -230,7 +231,6 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0;
 
-    const int nk = (int)((K + BK - 1) / BK);
     // Prologue: every LDS buffer gets a stage in flight.  The loop below issues one stage per
     // iteration unconditionally, so the number of DMAs in flight is always the same and every
     // wait is a compile-time constant; stages past the end of K only fetch zeros or unused bytes

@@ -12,6 +12,10 @@ Reference plugins mirrored (paths under operators/):
   grouped_matmul_swiglu_quant  groupedmatmulswigluquant/csrc/ops/grouped_matmul_swiglu_quant/op_plugin/gmsq_plugin.cpp:40-145
   quant_matmul                 quantmatmul/csrc/ops/quant_matmul/op_plugin/quant_matmul_plugin.cpp:48-267
   grouped_matmul_quant         (no reference op) group semantics of groupedmatmul/csrc/ops/grouped_matmul/op_plugin/grouped_matmul_plugin.cpp:42-185
+  moe_re_routing               moererouting/csrc/ops/moe_re_routing/op_plugin/moe_re_routing_plugin.cpp:33-160
+  moe_finalize_routing         moefinalizerouting/csrc/ops/moe_finalize_routing/op_plugin/moe_finalize_routing_plugin.cpp:31-215
+  dequant_swiglu_quant         dequantswigluquant/csrc/ops/dequant_swiglu_quant/op_plugin/dqsq_plugin.cpp:32-140
+  moe_gating_top_k_softmax     moegatingtopksoftmax/csrc/ops/moe_gating_top_k_softmax/op_plugin/moe_gating_plugin.cpp:28-115
 """
 import torch
 
@@ -49,7 +53,7 @@ def _raise_status(name, code):
 def _dtype_code(dt):
     return {torch.float16: L.CB_DT_FLOAT16, torch.bfloat16: L.CB_DT_BFLOAT16,
             torch.float32: L.CB_DT_FLOAT32, torch.int8: L.CB_DT_INT8,
-            torch.int32: L.CB_DT_INT32}.get(dt, -1)
+            torch.int32: L.CB_DT_INT32, torch.int64: L.CB_DT_INT64}.get(dt, -1)
 
 
 # ------------------------------------------------------------------------------------------------
@@ -309,3 +313,205 @@ def grouped_matmul_int32(x, weight, group_list):
     rc = L.load().cb_grouped_matmul_int32(_ptr(x), _ptr(weight), gla, len(gl), M, K, N, E, _ptr(c), _stream())
     _raise_status(name, rc)
     return c
+
+
+# ------------------------------------------------------------------------------------------------
+# MoeReRouting
+# ------------------------------------------------------------------------------------------------
+def moe_re_routing_meta(tokens, expert_token_num_per_rank, per_token_scales=None, expert_token_num_type=1,
+                        idx_type=0):
+    _check(tokens.dim() == 2, "moe_re_routing: tokens must be 2D (A, H).")
+    _check(expert_token_num_per_rank.dim() == 2, "moe_re_routing: expert_token_num_per_rank must be 2D (N, E).")
+    a, h = tokens.shape
+    e = expert_token_num_per_rank.size(1)
+    dev = tokens.device
+    return (torch.empty((a, h), dtype=tokens.dtype, device=dev),
+            torch.empty((a,), dtype=torch.float32, device=dev),
+            torch.empty((a,), dtype=torch.int32, device=dev),
+            torch.empty((e,), dtype=expert_token_num_per_rank.dtype, device=expert_token_num_per_rank.device))
+
+
+def moe_re_routing(tokens, expert_token_num_per_rank, per_token_scales=None, expert_token_num_type=1, idx_type=0):
+    """(permute_tokens, permute_per_token_scales, permute_token_idx, expert_token_num): rank-major tokens
+    re-ordered expert-major.  expert_token_num_type is accepted and ignored, as in the reference."""
+    _check(idx_type == 0, "moe_re_routing: only gather index mode (idx_type == 0) is supported.")
+    tokens = tokens.contiguous()
+    counts = expert_token_num_per_rank.contiguous()
+    has_scales = per_token_scales is not None
+    if has_scales:
+        per_token_scales = per_token_scales.contiguous()
+        _check(per_token_scales.dtype == torch.float32, "moe_re_routing: per_token_scales must be float32.")
+    outs = moe_re_routing_meta(tokens, counts, per_token_scales, expert_token_num_type, idx_type)
+    a, h = tokens.shape
+    n, e = counts.shape
+    if a <= 0 or h <= 0 or n <= 0 or e <= 0:
+        return outs
+    _check(tokens.dtype in (torch.float16, torch.bfloat16, torch.int8), "moe_re_routing: unsupported tokens dtype.")
+    _check(counts.dtype in (torch.int32, torch.int64),
+           "moe_re_routing: unsupported expert_token_num_per_rank dtype.")
+    if has_scales:
+        _check(per_token_scales.numel() == a, "moe_re_routing: per_token_scales must have A elements.")
+    _on_device("moe_re_routing", tokens, counts, per_token_scales)
+    pt, ps, pi, etn = outs
+    lib = L.load()
+    wsb = lib.cb_moe_re_routing_workspace_size(n, e)
+    ws = torch.empty((max(wsb, 1),), dtype=torch.uint8, device=tokens.device)
+    rc = lib.cb_moe_re_routing(_ptr(tokens), _dtype_code(tokens.dtype), a, h, _ptr(counts), _dtype_code(counts.dtype),
+                               n, e, _ptr(per_token_scales), _ptr(pt), _ptr(ps), _ptr(pi), _ptr(etn), _ptr(ws), wsb,
+                               _stream())
+    _raise_status("moe_re_routing", rc)
+    return outs
+
+
+# ------------------------------------------------------------------------------------------------
+# MoeFinalizeRouting
+# ------------------------------------------------------------------------------------------------
+def _mfr_resolve(epr, esdr, scales):
+    _check(epr.dim() >= 2, "moe_finalize_routing: expanded_permuted_rows must have rank >= 2.")
+    _check(esdr.dtype == torch.int32, "moe_finalize_routing: expanded_src_to_dst_row must be int32.")
+    H = epr.size(-1)
+    nk = esdr.numel()
+    K = 1
+    if scales is not None:
+        _check(scales.dim() == 2, "moe_finalize_routing: scales must be 2-D (NUM_ROWS, K).")
+        K = scales.size(1)
+    _check(K > 0, "moe_finalize_routing: K must be positive.")
+    _check(nk % K == 0, "moe_finalize_routing: expanded_src_to_dst_row length must be K*NUM_ROWS.")
+    return nk // K, K, H
+
+
+def moe_finalize_routing_meta(expanded_permuted_rows, expanded_src_to_dst_row, skip1=None, skip2=None, bias=None,
+                              scales=None, expert_for_source_row=None, drop_pad_mode=0):
+    num_rows, _, H = _mfr_resolve(expanded_permuted_rows, expanded_src_to_dst_row, scales)
+    return torch.empty((num_rows, H), dtype=expanded_permuted_rows.dtype, device=expanded_permuted_rows.device)
+
+
+_FLOATS = (torch.float16, torch.float32, torch.bfloat16)
+
+
+def moe_finalize_routing(expanded_permuted_rows, expanded_src_to_dst_row, skip1=None, skip2=None, bias=None,
+                         scales=None, expert_for_source_row=None, drop_pad_mode=0):
+    """out [NUM_ROWS, H] = skip1 + skip2 + sum_k scales[:, k] * (epr[p(i, k)] + bias[expert[i, k]])."""
+    name = "moe_finalize_routing"
+    _check(expanded_permuted_rows.dtype in _FLOATS,
+           f"{name}: expanded_permuted_rows must be float16 / float32 / bfloat16.")
+    epr = expanded_permuted_rows.contiguous()
+    esdr = expanded_src_to_dst_row.contiguous()
+    num_rows, K, H = _mfr_resolve(epr, esdr, scales)
+    out = torch.empty((num_rows, H), dtype=epr.dtype, device=epr.device)
+    if num_rows <= 0 or H <= 0 or K <= 0:
+        return out
+    num_dst = epr.numel() // H
+    has_bias = bias is not None and expert_for_source_row is not None
+    if has_bias:
+        _check(bias.size(1) == H, f"{name}: bias head dim must equal H.")
+    _check(scales is None or scales.dtype in _FLOATS,
+           f"{name}: unsupported dtype combination for expanded_permuted_rows / scales.")
+    sk1 = None if skip1 is None else skip1.contiguous()
+    sk2 = None if skip2 is None else skip2.contiguous()
+    bs = bias.contiguous() if has_bias else None
+    sc = None if scales is None else scales.contiguous()
+    ex = None if expert_for_source_row is None else expert_for_source_row.contiguous()
+    for t, what in ((sk1, "skip1"), (sk2, "skip2"), (bs, "bias")):
+        if t is not None:
+            _check(t.dtype == epr.dtype, f"{name}: {what} must have the dtype of expanded_permuted_rows.")
+    if sk1 is not None:
+        _check(sk1.numel() >= num_rows * H, f"{name}: skip1 must hold NUM_ROWS * H elements.")
+    if sk2 is not None:
+        _check(sk2.numel() >= num_rows * H, f"{name}: skip2 must hold NUM_ROWS * H elements.")
+    if ex is not None:
+        _check(ex.dtype == torch.int32, f"{name}: expert_for_source_row must be int32.")
+        _check(ex.numel() >= num_rows * K, f"{name}: expert_for_source_row must hold NUM_ROWS * K elements.")
+    _on_device(name, epr, esdr, sk1, sk2, bs, sc, ex)
+    rc = L.load().cb_moe_finalize_routing(
+        _ptr(epr), _dtype_code(epr.dtype), num_dst, H, _ptr(esdr), num_rows, K, _ptr(sk1), _ptr(sk2), _ptr(bs),
+        bs.size(0) if bs is not None else 0, _ptr(sc), _dtype_code(sc.dtype) if sc is not None else 0, _ptr(ex),
+        int(drop_pad_mode), _ptr(out), _stream())
+    _raise_status(name, rc)
+    return out
+
+
+# ------------------------------------------------------------------------------------------------
+# DequantSwigluQuant
+# ------------------------------------------------------------------------------------------------
+def dequant_swiglu_quant_meta(x, weight_scale=None, activation_scale=None, quant_scale=None, activate_left=False):
+    _check(x.dim() == 2, "dequant_swiglu_quant requires a 2D input [TokensNum, 2H].")
+    M, N2 = x.shape
+    _check(N2 % 2 == 0, "dequant_swiglu_quant requires an even last dimension.")
+    return (torch.empty((M, N2 // 2), dtype=torch.int8, device=x.device),
+            torch.empty((M,), dtype=torch.float32, device=x.device))
+
+
+def dequant_swiglu_quant(x, weight_scale=None, activation_scale=None, quant_scale=None, activate_left=False):
+    """(y int8 [M, H], scale fp32 [M]) = per-token quant of SwiGLU(dequant(x))."""
+    _check(x.dim() == 2, "dequant_swiglu_quant requires a 2D input [TokensNum, 2H].")
+    _check(x.is_contiguous(), "dequant_swiglu_quant requires a contiguous input.")
+    y, scale = dequant_swiglu_quant_meta(x, weight_scale, activation_scale, quant_scale, activate_left)
+    M, N2 = x.shape
+    if M <= 0 or N2 <= 0:
+        return y, scale
+    H = N2 // 2
+    if x.dtype == torch.int32:
+        _check(weight_scale is not None, "weight_scale is required when x is int32.")
+        _check(activation_scale is not None, "activation_scale is required when x is int32.")
+        _check(weight_scale.dtype == torch.float32, "weight_scale must be float32.")
+        _check(activation_scale.dtype == torch.float32, "activation_scale must be float32.")
+        _check(weight_scale.is_contiguous() and activation_scale.is_contiguous(),
+               "weight_scale / activation_scale must be contiguous.")
+        _check(weight_scale.numel() == N2, "weight_scale must have 2H elements.")
+        _check(activation_scale.numel() == M, "activation_scale must have TokensNum elements.")
+    else:
+        _check(x.dtype in (torch.float16, torch.bfloat16),
+               "dequant_swiglu_quant supports int32 / float16 / bfloat16 inputs.")
+        _check(weight_scale is None, "weight_scale must be None for float16 / bfloat16 inputs.")
+        _check(activation_scale is None, "activation_scale must be None for float16 / bfloat16 inputs.")
+    if quant_scale is not None:
+        _check(quant_scale.dtype == torch.float32, "quant_scale must be float32.")
+        _check(quant_scale.is_contiguous(), "quant_scale must be contiguous.")
+        _check(quant_scale.numel() == H, "quant_scale must have H elements.")
+    _on_device("dequant_swiglu_quant", x, weight_scale, activation_scale, quant_scale)
+    rc = L.load().cb_dequant_swiglu_quant(_ptr(x), _dtype_code(x.dtype), M, N2, _ptr(weight_scale),
+                                          _ptr(activation_scale), _ptr(quant_scale), int(bool(activate_left)),
+                                          _ptr(y), _ptr(scale), _stream())
+    _raise_status("dequant_swiglu_quant", rc)
+    return y, scale
+
+
+# ------------------------------------------------------------------------------------------------
+# MoeGatingTopKSoftmax
+# ------------------------------------------------------------------------------------------------
+_MGT = "cann_bench.moe_gating_top_k_softmax"
+
+
+def moe_gating_top_k_softmax_meta(x, finished=None, k=1):
+    _check(x.dtype in (torch.float32, torch.float16, torch.bfloat16),
+           f"{_MGT} only supports float32, float16 and bfloat16 inputs.")
+    _check(x.dim() >= 2, f"{_MGT} requires a tensor with rank >= 2.")
+    inner = x.size(-1)
+    _check(inner > 0, f"{_MGT} requires a non-empty last dimension.")
+    _check(0 < k <= inner, f"{_MGT} requires 0 < k <= x.size(-1).")
+    if finished is not None:
+        _check(finished.dtype == torch.bool, f"{_MGT} requires a bool 'finished' tensor.")
+    shape = tuple(x.shape[:-1]) + (k,)
+    return (torch.empty(shape, dtype=x.dtype, device=x.device),
+            torch.empty(shape, dtype=torch.int32, device=x.device),
+            torch.empty(shape, dtype=torch.int32, device=x.device))
+
+
+def moe_gating_top_k_softmax(x, finished=None, k=1):
+    """(y, expert_idx int32, row_idx int32) = top-k of softmax(x, -1); finished rows get expert E."""
+    xc = x.contiguous()
+    y, ei, ri = moe_gating_top_k_softmax_meta(xc, finished, k)
+    inner = xc.size(-1)
+    rows = xc.numel() // inner
+    _check(rows > 0, f"{_MGT} requires at least one row.")
+    fin = None
+    if finished is not None:
+        fin = finished.contiguous()
+        _check(fin.numel() == rows, f"{_MGT}: finished must have numel == rows.")
+    _check(inner <= 2048, f"{_MGT}: the last dimension must not exceed 2048 on this device.")
+    _on_device("moe_gating_top_k_softmax", xc, fin)
+    rc = L.load().cb_moe_gating_top_k_softmax(_ptr(xc), _dtype_code(xc.dtype), rows, inner, _ptr(fin), k, _ptr(y),
+                                              _ptr(ei), _ptr(ri), _stream())
+    _raise_status("moe_gating_top_k_softmax", rc)
+    return y, ei, ri

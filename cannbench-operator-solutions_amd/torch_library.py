@@ -22,6 +22,14 @@ SCHEMAS = {
         "quant_matmul(Tensor x1, Tensor x2, Tensor scale, *, Tensor? offset=None, Tensor? pertoken_scale=None, Tensor? bias=None, str? output_dtype=None) -> Tensor",
     "grouped_matmul_quant":
         "grouped_matmul_quant(Tensor x, Tensor weight, Tensor weight_scale, Tensor x_scale, int[] group_list) -> Tensor",
+    "moe_re_routing":
+        "moe_re_routing(Tensor tokens, Tensor expert_token_num_per_rank, Tensor? per_token_scales=None, int expert_token_num_type=1, int idx_type=0) -> (Tensor, Tensor, Tensor, Tensor)",
+    "moe_finalize_routing":
+        "moe_finalize_routing(Tensor expanded_permuted_rows, Tensor expanded_src_to_dst_row, Tensor? skip1=None, Tensor? skip2=None, Tensor? bias=None, Tensor? scales=None, Tensor? expert_for_source_row=None, int drop_pad_mode=0) -> Tensor out",
+    "dequant_swiglu_quant":
+        "dequant_swiglu_quant(Tensor x, Tensor? weight_scale=None, Tensor? activation_scale=None, Tensor? quant_scale=None, bool activate_left=False) -> (Tensor y, Tensor scale)",
+    "moe_gating_top_k_softmax":
+        "moe_gating_top_k_softmax(Tensor x, Tensor? finished=None, int k=1) -> (Tensor y, Tensor expert_idx, Tensor row_idx)",
 }
 
 _IMPLS = {
@@ -32,6 +40,10 @@ _IMPLS = {
                      lambda x1, x2, scale, *, offset=None, pertoken_scale=None, bias=None, output_dtype=None:
                      ops.quant_matmul_meta(x1, x2, scale, offset, pertoken_scale, bias, output_dtype)),
     "grouped_matmul_quant": (ops.grouped_matmul_quant, ops.grouped_matmul_quant_meta),
+    "moe_re_routing": (ops.moe_re_routing, ops.moe_re_routing_meta),
+    "moe_finalize_routing": (ops.moe_finalize_routing, ops.moe_finalize_routing_meta),
+    "dequant_swiglu_quant": (ops.dequant_swiglu_quant, ops.dequant_swiglu_quant_meta),
+    "moe_gating_top_k_softmax": (ops.moe_gating_top_k_softmax, ops.moe_gating_top_k_softmax_meta),
 }
 
 _lib_def = None

@@ -55,7 +55,8 @@ typedef enum cb_dtype {
     CB_DT_BFLOAT16 = 2,
     CB_DT_FLOAT32 = 3,
     CB_DT_INT8 = 4,
-    CB_DT_INT32 = 5
+    CB_DT_INT32 = 5,
+    CB_DT_INT64 = 6
 } cb_dtype;
 
 /* Largest expert count accepted by the grouped operators (the reference accepts 64:
@@ -175,6 +176,81 @@ int cb_grouped_matmul_quant(const int8_t* x, const int8_t* weight, const float* 
 int cb_grouped_matmul_int32(const int8_t* x, const int8_t* weight, const int64_t* group_list,
                             int64_t group_len, int64_t M, int64_t K, int64_t N, int64_t E, int32_t* c,
                             void* stream);
+
+/* ----------------------------------------------------------------------------------------------
+ * Routing operators on either side of the expert FFN.
+ * ---------------------------------------------------------------------------------------------- */
+
+/* Workspace bytes cb_moe_re_routing needs for an [n_ranks, n_experts] count matrix. */
+int64_t cb_moe_re_routing_workspace_size(int64_t n_ranks, int64_t n_experts);
+
+/*
+ * MoeReRouting: permute tokens received from n_ranks ranks (rank-major, each rank's block expert
+ * ordered) into expert-major order.  Replaces moe_re_routing(tokens, expert_token_num_per_rank,
+ * per_token_scales, expert_token_num_type, idx_type)
+ * (operators/moererouting/csrc/ops/moe_re_routing/op_plugin/moe_re_routing_plugin.cpp:35-38,
+ *  semantics op_kernel/moe_re_routing_kernel.cpp:15-24; only idx_type 0 exists there).
+ *   tokens [A, H] (CB_DT_FLOAT16 / CB_DT_BFLOAT16 / CB_DT_INT8), counts [n_ranks, n_experts]
+ *   (CB_DT_INT32 / CB_DT_INT64), per_token_scales fp32 [A] or NULL.
+ *   Outputs: permute_tokens [A, H], permute_scales fp32 [A] (0 without scales), permute_idx int32 [A]
+ *   (source row of each output row), expert_token_num [n_experts] (counts dtype; column sums).
+ *   Rows past sum(counts) are left unwritten, as in the reference.  Any zero dimension returns CB_OK
+ *   without writing (plugin :103-105).  n_ranks <= 1024.
+ */
+int cb_moe_re_routing(const void* tokens, int tokens_dtype, int64_t A, int64_t H, const void* counts,
+                      int counts_dtype, int64_t n_ranks, int64_t n_experts, const float* per_token_scales,
+                      void* permute_tokens, float* permute_scales, int32_t* permute_idx, void* expert_token_num,
+                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * MoeFinalizeRouting: combine the K expert outputs of each token.  Replaces
+ * moe_finalize_routing(expanded_permuted_rows, expanded_src_to_dst_row, skip1, skip2, bias, scales,
+ * expert_for_source_row, drop_pad_mode)
+ * (operators/moefinalizerouting/csrc/ops/moe_finalize_routing/op_plugin/moe_finalize_routing_plugin.cpp:33-36,
+ *  semantics op_kernel/moe_finalize_routing_kernel.cpp:14-25):
+ *   out[i, c] = skip1[i, c] + skip2[i, c] + sum_k scales[i, k] * (epr[p(i, k), c] + bias[eid(i, k), c])
+ *   p(i, k) = esdr[k * num_rows + i] (drop_pad_mode 0/1) or esdr[i * K + k] (2/3); modes clamp to [0, 3];
+ *   p outside [0, num_dst) drops the term; eid = expert_for_source_row[i * K + k] outside [0, n_bias_rows)
+ *   drops only the bias.  Bias is used only together with expert_for_source_row.  fp32 accumulation in
+ *   ascending k, round-half-even store.
+ *   dtype: CB_DT_FLOAT16 / CB_DT_BFLOAT16 / CB_DT_FLOAT32 for epr, skips, bias and out; scales may be
+ *   any of the three (scales_dtype) or NULL (then K is the caller's, normally 1).
+ */
+int cb_moe_finalize_routing(const void* expanded_permuted_rows, int dtype, int64_t num_dst, int64_t H,
+                            const int32_t* expanded_src_to_dst_row, int64_t num_rows, int64_t K,
+                            const void* skip1, const void* skip2, const void* bias, int64_t n_bias_rows,
+                            const void* scales, int scales_dtype, const int32_t* expert_for_source_row,
+                            int drop_pad_mode, void* out, void* stream);
+
+/*
+ * DequantSwigluQuant: dequant + SwiGLU + per-token int8 quantisation of an [M, 2H] row block.  Replaces
+ * dequant_swiglu_quant(x, weight_scale, activation_scale, quant_scale, activate_left)
+ * (operators/dequantswigluquant/csrc/ops/dequant_swiglu_quant/op_plugin/dqsq_plugin.cpp:34-35,
+ *  operation order op_kernel/dqsq_kernel.cpp:334-427):
+ *   A = x[:, :H], B = x[:, H:] as fp32; int32 x: A *= weight_scale[:H], B *= weight_scale[H:];
+ *   quant_scale [H] multiplies the non-gate half; int32 x: A, B *= activation_scale[row];
+ *   out = (A * B) / (1 + exp(-G)), G = B (activate_left 0) or A (activate_left 1);
+ *   scale[row] = max(max|out| * (1/127), 1e-12); y = int8(rint(half(clamp(out / scale, -128, 127)))).
+ *   x_dtype CB_DT_INT32 (weight_scale [2H] and activation_scale [M] required) or CB_DT_FLOAT16 /
+ *   CB_DT_BFLOAT16 (both must be NULL).  y int8 [M, H], scale fp32 [M].
+ */
+int cb_dequant_swiglu_quant(const void* x, int x_dtype, int64_t M, int64_t N2, const float* weight_scale,
+                            const float* activation_scale, const float* quant_scale, int activate_left,
+                            int8_t* y, float* scale, void* stream);
+
+/*
+ * MoeGatingTopKSoftmax: fp32 softmax over the last dimension and its top k.  Replaces
+ * moe_gating_top_k_softmax(x, finished, k)
+ * (operators/moegatingtopksoftmax/csrc/ops/moe_gating_top_k_softmax/op_plugin/moe_gating_plugin.cpp:30,
+ *  semantics op_kernel/moe_gating_kernel.cpp:15-21):
+ *   y [rows, k] (x dtype) = the k largest softmax values in descending order (ties: lower column first);
+ *   expert_idx int32 [rows, k] = their columns, or E for rows with finished[r] != 0;
+ *   row_idx int32 [rows, k]: row_idx[r, j] = j * rows + r.
+ *   x [rows, E] CB_DT_FLOAT32 / CB_DT_FLOAT16 / CB_DT_BFLOAT16, finished uint8/bool [rows] or NULL,
+ *   0 < k <= E <= 2048.
+ */
+int cb_moe_gating_top_k_softmax(const void* x, int dtype, int64_t rows, int64_t E, const uint8_t* finished,
+                                int64_t k, void* y, int32_t* expert_idx, int32_t* row_idx, void* stream);
 
 #ifdef __cplusplus
 }

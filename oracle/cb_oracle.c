@@ -17,6 +17,10 @@
  *   or_grouped_matmul_quant  group routing of operators/groupedmatmul/.../op_plugin/grouped_matmul_plugin.cpp:82-95
  *                      with the QuantMatmul epilogue order (no reference op exists: parity unpinned by the
  *                      reference, pinned here only by the closed forms the tests check)
+ *   or_moe_re_routing        operators/moererouting/.../op_kernel/moe_re_routing_kernel.cpp:15-24
+ *   or_moe_finalize_routing  operators/moefinalizerouting/.../op_kernel/moe_finalize_routing_kernel.cpp:14-25,137-183
+ *   or_dequant_swiglu_quant  operators/dequantswigluquant/.../op_kernel/dqsq_kernel.cpp:15-27,334-427,476-524
+ *   or_moe_gating_top_k_softmax  operators/moegatingtopksoftmax/.../op_kernel/moe_gating_kernel.cpp:15-21,318-390
  *
  * Rounding conventions (all round-half-to-even):
  *   rint16(v)  fp32 -> fp16 -> int8, the reference's two-step narrowing (dynamic_quant_kernel.cpp:20-22,
@@ -325,4 +329,164 @@ void or_grouped_matmul_quant(const int8_t* x, const int8_t* w, const float* ws, 
         r = gend;
     }
     free(c);
+}
+
+/* ============================================================================================
+ * Routing operators on either side of the expert FFN.
+ * ============================================================================================ */
+
+/* MoeReRouting (operators/moererouting/csrc/ops/moe_re_routing/op_kernel/moe_re_routing_kernel.cpp:15-24):
+ * the (rank i, expert j) cell's cnt[i][j] rows move from source offset
+ * rowStart(i) + sum_{j'<j} cnt[i][j'] to destination offset colStart(j) + sum_{i'<i} cnt[i'][j].
+ * Written as the direct double loop over cells, in the order of that definition.
+ * counts are int64 here (the wrapper widens int32).  Returns the routed total. */
+int64_t or_moe_re_routing(const uint8_t* tokens, int64_t A, int64_t row_bytes, const int64_t* cnt,
+                          int64_t n, int64_t e, const float* scales, uint8_t* out_tok, float* out_sc,
+                          int32_t* out_idx, int64_t* etn)
+{
+    int64_t* dst = (int64_t*)malloc(sizeof(int64_t) * (size_t)(e > 0 ? e : 1));
+    int64_t run = 0;
+    for (int64_t j = 0; j < e; ++j) {
+        int64_t col = 0;
+        for (int64_t i = 0; i < n; ++i) col += cnt[i * e + j];
+        etn[j] = col;
+        dst[j] = run; /* colStart(j), advanced by each rank's count below */
+        run += col;
+    }
+    int64_t src = 0; /* rowStart(i) + sum_{j'<j} cnt[i][j'] */
+    for (int64_t i = 0; i < n; ++i) {
+        for (int64_t j = 0; j < e; ++j) {
+            const int64_t c = cnt[i * e + j];
+            for (int64_t k = 0; k < c; ++k) {
+                const int64_t s = src + k, d = dst[j] + k;
+                if (s < 0 || s >= A || d < 0 || d >= A) continue;
+                memcpy(out_tok + d * row_bytes, tokens + s * row_bytes, (size_t)row_bytes);
+                out_sc[d] = scales ? scales[s] : 0.0f;
+                out_idx[d] = (int32_t)s;
+            }
+            src += c;
+            dst[j] += c;
+        }
+    }
+    free(dst);
+    return run;
+}
+
+/* MoeFinalizeRouting (operators/moefinalizerouting/csrc/ops/moe_finalize_routing/op_kernel/
+ * moe_finalize_routing_kernel.cpp:14-25, 137-183): fp32 accumulation, ascending k, RNE store.
+ * Null skip / bias / scales / expert pointers mean absent. */
+void or_moe_finalize_routing(const void* epr, int dtype, int64_t num_dst, int64_t H, const int32_t* esdr,
+                             int64_t num_rows, int64_t K, const void* skip1, const void* skip2,
+                             const void* bias, int64_t n_bias, const void* scales, int scales_dtype,
+                             const int32_t* expert, int mode, void* out)
+{
+    if (mode < 0) mode = 0;
+    if (mode > 3) mode = 3;
+    if (!expert) bias = NULL;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < num_rows; ++i) {
+        for (int64_t c = 0; c < H; ++c) {
+            float acc = 0.0f;
+            if (skip1) acc = load_any(skip1, dtype, i * H + c);
+            if (skip2) acc = acc + load_any(skip2, dtype, i * H + c);
+            for (int64_t k = 0; k < K; ++k) {
+                const int64_t p = esdr[mode <= 1 ? k * num_rows + i : i * K + k];
+                if (p < 0 || p >= num_dst) continue;
+                float term = load_any(epr, dtype, p * H + c);
+                if (bias) {
+                    const int64_t eid = expert[i * K + k];
+                    if (eid >= 0 && eid < n_bias) term = term + load_any(bias, dtype, eid * H + c);
+                }
+                if (scales) term = term * load_any(scales, scales_dtype, i * K + k);
+                acc = acc + term;
+            }
+            if (dtype == DT_F32) ((float*)out)[i * H + c] = acc;
+            else ((uint16_t*)out)[i * H + c] = store16(acc, dtype);
+        }
+    }
+}
+
+/* DequantSwigluQuant (operators/dequantswigluquant/csrc/ops/dequant_swiglu_quant/op_kernel/
+ * dqsq_kernel.cpp:15-27, 334-427, 476-524).  x is int32 / fp16 / bf16 [M, 2H]. */
+void or_dequant_swiglu_quant(const void* x, int x_dtype, int64_t M, int64_t H, const float* ws,
+                             const float* as, const float* qs, int act_left, int8_t* y, float* scale)
+{
+#pragma omp parallel
+    {
+        float* out = (float*)malloc(sizeof(float) * (size_t)(H > 0 ? H : 1));
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < M; ++r) {
+            float amax = 0.0f;
+            for (int64_t j = 0; j < H; ++j) {
+                float A = load_any(x, x_dtype, r * 2 * H + j), B = load_any(x, x_dtype, r * 2 * H + H + j);
+                if (x_dtype == DT_I32) {
+                    A = A * ws[j];
+                    B = B * ws[H + j];
+                }
+                if (qs) {
+                    if (act_left) B = B * qs[j];
+                    else A = A * qs[j];
+                }
+                if (x_dtype == DT_I32) {
+                    A = A * as[r];
+                    B = B * as[r];
+                }
+                const float G = act_left ? A : B;
+                out[j] = (A * B) / (1.0f + expf(-G));
+                const float a = fabsf(out[j]);
+                if (a > amax) amax = a;
+            }
+            float s = amax * (1.0f / 127.0f);
+            if (!(s >= 1e-12f)) s = 1e-12f;
+            scale[r] = s;
+            for (int64_t j = 0; j < H; ++j) {
+                float q = out[j] / s;
+                q = q > 127.0f ? 127.0f : (q < -128.0f ? -128.0f : q);
+                y[r * H + j] = or_rint16(q);
+            }
+        }
+        free(out);
+    }
+}
+
+/* MoeGatingTopKSoftmax (operators/moegatingtopksoftmax/csrc/ops/moe_gating_top_k_softmax/op_kernel/
+ * moe_gating_kernel.cpp:15-21, 318-390): e = exp(x - max) in fp32, sum = sum(e); the k largest e in
+ * descending order (equal values: lower column first, the order of a stable sort), y = e / sum narrowed
+ * RNE to the x dtype; expert_idx = column (E for finished rows); row_idx = j * rows + r.
+ * Selection is k passes of a linear arg-max scan, so it is a brute-force restatement of the sort. */
+void or_moe_gating_top_k_softmax(const void* x, int dtype, int64_t rows, int64_t E, const uint8_t* finished,
+                                 int64_t k, void* y, int32_t* eidx, int32_t* ridx)
+{
+#pragma omp parallel
+    {
+        float* e = (float*)malloc(sizeof(float) * (size_t)E);
+        uint8_t* used = (uint8_t*)malloc((size_t)E);
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < rows; ++r) {
+            float m = -INFINITY;
+            for (int64_t c = 0; c < E; ++c) {
+                e[c] = load_any(x, dtype, r * E + c);
+                if (e[c] > m) m = e[c];
+            }
+            float s = 0.0f;
+            for (int64_t c = 0; c < E; ++c) {
+                e[c] = expf(e[c] - m);
+                used[c] = 0;
+            }
+            for (int64_t c = 0; c < E; ++c) s += e[c];
+            for (int64_t j = 0; j < k; ++j) {
+                int64_t b = -1;
+                for (int64_t c = 0; c < E; ++c)
+                    if (!used[c] && (b < 0 || e[c] > e[b])) b = c;
+                used[b] = 1;
+                const float v = e[b] / s;
+                if (dtype == DT_F32) ((float*)y)[r * k + j] = v;
+                else ((uint16_t*)y)[r * k + j] = store16(v, dtype);
+                eidx[r * k + j] = (finished && finished[r]) ? (int32_t)E : (int32_t)b;
+                ridx[r * k + j] = (int32_t)(j * rows + r);
+            }
+        }
+        free(e);
+        free(used);
+    }
 }

@@ -13,7 +13,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "_build", "libcb_oracle.so")
 
-DT = {"f16": 1, "bf16": 2, "f32": 3, "i8": 4, "i32": 5}
+DT = {"f16": 1, "bf16": 2, "f32": 3, "i8": 4, "i32": 5, "i64": 6}
 
 _lib = None
 
@@ -36,6 +36,11 @@ def lib():
         L.or_gmsq.argtypes = [P, P, P, P, P, I64, I64, I64, I64, I64, I64, P, P]
         L.or_quant_matmul.argtypes = [P, P, P, I, I64, P, I64, P, I64, P, I, I64, I, I64, I64, I64, I64, I, P, I64, I64]
         L.or_grouped_matmul_quant.argtypes = [P, P, P, P, P, I64, I64, I64, I64, I64, I64, P]
+        L.or_moe_re_routing.argtypes = [P, I64, I64, P, I64, I64, P, P, P, P, P]
+        L.or_moe_re_routing.restype = I64
+        L.or_moe_finalize_routing.argtypes = [P, I, I64, I64, P, I64, I64, P, P, P, I64, P, I, P, I, P]
+        L.or_dequant_swiglu_quant.argtypes = [P, I, I64, I64, P, P, P, I, P, P]
+        L.or_moe_gating_top_k_softmax.argtypes = [P, I, I64, I64, P, I64, P, P, P]
         L.or_rint16.argtypes = [F]
         L.or_rint16.restype = ctypes.c_int8
         L.or_f32_to_f16.argtypes = [F]
@@ -152,6 +157,76 @@ def grouped_matmul_quant(x, w, ws, xs, group_list, row_begin=0, row_end=None):
     out = np.zeros((M, N), np.uint16)
     lib().or_grouped_matmul_quant(_p(x), _p(w), _p(ws), _p(xs), _p(gl), E, M, K, N, row_begin, row_end, _p(out))
     return out
+
+
+# ---- routing operators -------------------------------------------------------------------------
+_NP = {"f16": np.uint16, "bf16": np.uint16, "f32": np.float32, "i32": np.int32, "i8": np.int8}
+
+
+def moe_re_routing(tokens, counts, scales=None):
+    """tokens [A, H] any 1/2-byte dtype (raw bytes are moved); counts [N, E] int.  Returns
+    (permute_tokens, permute_scales, permute_idx, expert_token_num, routed_total).  Rows past the
+    routed total are zero here (the operator leaves them unwritten)."""
+    t = np.ascontiguousarray(tokens)
+    A, H = t.shape
+    cnt = _c(counts, np.int64)
+    n, e = cnt.shape
+    sc = None if scales is None else _c(scales, np.float32)
+    out = np.zeros_like(t)
+    osc = np.zeros((A,), np.float32)
+    oidx = np.zeros((A,), np.int32)
+    etn = np.zeros((e,), np.int64)
+    total = lib().or_moe_re_routing(_p(t), A, H * t.itemsize, _p(cnt), n, e, _p(sc), _p(out), _p(osc), _p(oidx),
+                                    _p(etn))
+    return out, osc, oidx, etn, int(total)
+
+
+def moe_finalize_routing(epr, dtype, esdr, K, skip1=None, skip2=None, bias=None, scales=None, scales_dtype=None,
+                         expert=None, drop_pad_mode=0):
+    """epr [num_dst, H] (uint16 bits for f16/bf16, float32 for f32); esdr int32 [num_rows * K]."""
+    epr = _c(epr, _NP[dtype])
+    H = epr.shape[-1]
+    num_dst = epr.size // H
+    esdr = _c(esdr, np.int32)
+    num_rows = esdr.size // K
+    sk1 = None if skip1 is None else _c(skip1, _NP[dtype])
+    sk2 = None if skip2 is None else _c(skip2, _NP[dtype])
+    bi = None if bias is None else _c(bias, _NP[dtype])
+    sdt = scales_dtype or dtype
+    sc = None if scales is None else _c(scales, _NP[sdt])
+    ex = None if expert is None else _c(expert, np.int32)
+    out = np.zeros((num_rows, H), _NP[dtype])
+    lib().or_moe_finalize_routing(_p(epr), DT[dtype], num_dst, H, _p(esdr), num_rows, K, _p(sk1), _p(sk2), _p(bi),
+                                  0 if bi is None else bi.shape[0], _p(sc), DT[sdt], _p(ex), int(drop_pad_mode),
+                                  _p(out))
+    return out
+
+
+def dequant_swiglu_quant(x, x_dtype, weight_scale=None, activation_scale=None, quant_scale=None,
+                         activate_left=False):
+    x = _c(x, _NP[x_dtype])
+    M, N2 = x.shape
+    H = N2 // 2
+    ws = None if weight_scale is None else _c(weight_scale, np.float32)
+    asc = None if activation_scale is None else _c(activation_scale, np.float32)
+    qs = None if quant_scale is None else _c(quant_scale, np.float32)
+    y = np.zeros((M, H), np.int8)
+    s = np.zeros((M,), np.float32)
+    lib().or_dequant_swiglu_quant(_p(x), DT[x_dtype], M, H, _p(ws), _p(asc), _p(qs), int(bool(activate_left)),
+                                  _p(y), _p(s))
+    return y, s
+
+
+def moe_gating_top_k_softmax(x, dtype, k, finished=None):
+    x = _c(x, _NP[dtype])
+    E = x.shape[-1]
+    rows = x.size // E
+    fin = None if finished is None else _c(finished, np.uint8)
+    y = np.zeros((rows, k), _NP[dtype])
+    ei = np.zeros((rows, k), np.int32)
+    ri = np.zeros((rows, k), np.int32)
+    lib().or_moe_gating_top_k_softmax(_p(x), DT[dtype], rows, E, _p(fin), k, _p(y), _p(ei), _p(ri))
+    return y, ei, ri
 
 
 # ---- 16-bit helpers ----------------------------------------------------------------------------

@@ -122,3 +122,34 @@ def test_norm_quant_validation(lib):
     assert so.cb_add_rms_norm_dynamic_quant(FAKE, FAKE, FAKE, 2, 0, 64, 1e-6, FAKE, FAKE, FAKE, None) == L.CB_OK
     assert so.cb_dynamic_quant(FAKE, 4, 4, 64, FAKE, FAKE, None) == L.CB_ERR_DTYPE
     assert so.cb_dynamic_quant(FAKE, 1, 4, 0, FAKE, FAKE, None) == L.CB_ERR_EMPTY
+
+
+def test_routing_validation(lib):
+    L, so = lib
+    # MoeReRouting: zero dimensions return before any dtype check (reference plugin order)
+    assert so.cb_moe_re_routing(FAKE, 9, 0, 16, FAKE, 9, 2, 2, None, FAKE, FAKE, FAKE, FAKE, None, 0, None) == L.CB_OK
+    assert so.cb_moe_re_routing(FAKE, 3, 4, 16, FAKE, 5, 2, 2, None, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 20, None) \
+        == L.CB_ERR_DTYPE
+    assert so.cb_moe_re_routing(FAKE, 2, 4, 16, FAKE, 4, 2, 2, None, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 20, None) \
+        == L.CB_ERR_DTYPE
+    assert so.cb_moe_re_routing(FAKE, 2, 4, 16, FAKE, 6, 2, 2, None, FAKE, FAKE, FAKE, FAKE, FAKE, 8, None) \
+        == L.CB_ERR_WORKSPACE
+    assert so.cb_moe_re_routing_workspace_size(2, 2) >= 2 * 2 * 4 * 2 + 3 * 4
+    assert so.cb_moe_re_routing_workspace_size(0, 2) == 0
+    # MoeFinalizeRouting
+    assert so.cb_moe_finalize_routing(FAKE, 4, 4, 8, FAKE, 2, 1, None, None, None, 0, None, 0, None, 0, FAKE, None) \
+        == L.CB_ERR_DTYPE
+    assert so.cb_moe_finalize_routing(FAKE, 2, 4, 8, FAKE, 2, 0, None, None, None, 0, None, 0, None, 0, FAKE, None) \
+        == L.CB_ERR_SHAPE
+    assert so.cb_moe_finalize_routing(FAKE, 2, 4, 8, FAKE, 0, 1, None, None, None, 0, None, 0, None, 0, FAKE, None) \
+        == L.CB_OK
+    # DequantSwigluQuant
+    assert so.cb_dequant_swiglu_quant(FAKE, 2, 4, 7, None, None, None, 0, FAKE, FAKE, None) == L.CB_ERR_N_ODD
+    assert so.cb_dequant_swiglu_quant(FAKE, 5, 4, 8, None, FAKE, None, 0, FAKE, FAKE, None) == L.CB_ERR_NULL_POINTER
+    assert so.cb_dequant_swiglu_quant(FAKE, 2, 4, 8, FAKE, None, None, 0, FAKE, FAKE, None) == L.CB_ERR_SCALE_LEN
+    assert so.cb_dequant_swiglu_quant(FAKE, 3, 4, 8, None, None, None, 0, FAKE, FAKE, None) == L.CB_ERR_DTYPE
+    # MoeGatingTopKSoftmax
+    assert so.cb_moe_gating_top_k_softmax(FAKE, 4, 4, 8, None, 2, FAKE, FAKE, FAKE, None) == L.CB_ERR_DTYPE
+    assert so.cb_moe_gating_top_k_softmax(FAKE, 3, 4, 8, None, 9, FAKE, FAKE, FAKE, None) == L.CB_ERR_SHAPE
+    assert so.cb_moe_gating_top_k_softmax(FAKE, 3, 4, 4096, None, 2, FAKE, FAKE, FAKE, None) == L.CB_ERR_SHAPE
+    assert so.cb_moe_gating_top_k_softmax(FAKE, 3, 0, 8, None, 2, FAKE, FAKE, FAKE, None) == L.CB_ERR_EMPTY

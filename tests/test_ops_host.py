@@ -90,3 +90,47 @@ def test_torch_ops_meta_shapes(cb):
                                                     torch.empty(2, 32, 48, dtype=torch.int8, device=m),
                                                     torch.empty(2, 48, device=m), torch.empty(6, device=m), [2, 6])
     assert out.shape == (6, 48) and out.dtype == torch.bfloat16
+
+
+def test_routing_checks_and_meta(cb):
+    with pytest.raises(RuntimeError, match="only gather index mode"):
+        cb.moe_re_routing(torch.zeros(4, 8, dtype=torch.bfloat16), torch.ones(2, 2, dtype=torch.int32), idx_type=1)
+    with pytest.raises(RuntimeError, match="tokens must be 2D"):
+        cb.moe_re_routing(torch.zeros(4, dtype=torch.bfloat16), torch.ones(2, 2, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="per_token_scales must be float32"):
+        cb.moe_re_routing(torch.zeros(4, 8, dtype=torch.bfloat16), torch.ones(2, 2, dtype=torch.int32),
+                          torch.zeros(4, dtype=torch.float16))
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        cb.moe_re_routing(torch.zeros(4, 8, dtype=torch.bfloat16), torch.ones(2, 2, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="must be int32"):
+        cb.moe_finalize_routing(torch.zeros(4, 8), torch.zeros(4, dtype=torch.int64))
+    with pytest.raises(RuntimeError, match="length must be K\\*NUM_ROWS"):
+        cb.moe_finalize_routing(torch.zeros(4, 8), torch.zeros(5, dtype=torch.int32), scales=torch.zeros(2, 2))
+    with pytest.raises(RuntimeError, match="float16 / float32 / bfloat16"):
+        cb.moe_finalize_routing(torch.zeros(4, 8, dtype=torch.int32), torch.zeros(4, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="activation_scale is required"):
+        cb.dequant_swiglu_quant(torch.zeros(2, 8, dtype=torch.int32), torch.zeros(8))
+    with pytest.raises(RuntimeError, match="weight_scale must be None"):
+        cb.dequant_swiglu_quant(torch.zeros(2, 8, dtype=torch.bfloat16), torch.zeros(8))
+    with pytest.raises(RuntimeError, match="quant_scale must have H elements"):
+        cb.dequant_swiglu_quant(torch.zeros(2, 8, dtype=torch.bfloat16), quant_scale=torch.zeros(3))
+    with pytest.raises(RuntimeError, match="0 < k <= x.size"):
+        cb.moe_gating_top_k_softmax(torch.zeros(2, 8), None, 9)
+    with pytest.raises(RuntimeError, match="bool 'finished'"):
+        cb.moe_gating_top_k_softmax(torch.zeros(2, 8), torch.zeros(2), 1)
+    with pytest.raises(RuntimeError, match="rank >= 2"):
+        cb.moe_gating_top_k_softmax(torch.zeros(8), None, 1)
+    cb.register_torch_ops()
+    m = torch.device("meta")
+    outs = torch.ops.cann_bench.moe_re_routing(torch.empty(10, 32, dtype=torch.int8, device=m),
+                                               torch.empty(4, 6, dtype=torch.int64, device=m))
+    assert [tuple(o.shape) for o in outs] == [(10, 32), (10,), (10,), (6,)]
+    assert outs[3].dtype == torch.int64 and outs[2].dtype == torch.int32
+    out = torch.ops.cann_bench.moe_finalize_routing(torch.empty(24, 16, dtype=torch.bfloat16, device=m),
+                                                    torch.empty(24, dtype=torch.int32, device=m),
+                                                    scales=torch.empty(3, 8, device=m))
+    assert out.shape == (3, 16) and out.dtype == torch.bfloat16
+    y, s = torch.ops.cann_bench.dequant_swiglu_quant(torch.empty(5, 64, dtype=torch.int32, device=m))
+    assert y.shape == (5, 32) and y.dtype == torch.int8 and s.shape == (5,)
+    y, ei, ri = torch.ops.cann_bench.moe_gating_top_k_softmax(torch.empty(2, 7, 64, device=m), None, 8)
+    assert y.shape == (2, 7, 8) and ei.dtype == torch.int32 and ri.dtype == torch.int32
