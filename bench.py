@@ -3,8 +3,9 @@
 Headline (`value`): GroupedMatmulSwigluQuant on the prefill configuration (131072 int8 rows,
 256 experts, K 7168, N 4096, Zipf(1.1) routing), in TOPS = 2*M*K*N / wall time of the whole op
 (all of its kernels), inputs resident in HBM.  The same JSON line also carries the decode
-configuration (GB/s of algorithmic bytes), its down-projection, AddRmsNormDynamicQuant and the
-dense QuantMatmul, each with its own roofline figure, plus a CPU baseline (the C oracle on a
+configuration (GB/s of algorithmic bytes), its down-projection, AddRmsNormDynamicQuant, the
+dense QuantMatmul and the routing operators (gating, re-routing, finalize, DequantSwigluQuant),
+each with its own roofline figure, plus a CPU baseline (the C oracle on a
 bounded sample of the prefill rows, on the host cores).
 
 A step is one operator call over one batch of synthetic input.  Usage:
@@ -134,9 +135,11 @@ def bench_ardq(steps, warmup, dev):
     R, H = d["x1"].shape
     nbytes = 2 * (2 * R * H) + 2 * H + 2 * R * H + R * H + 4 * R
     fn = lambda: cb.add_rms_norm_dynamic_quant(d["x1"], d["x2"], d["gamma"], d["epsilon"])
-    ms = time_op(fn, steps, warmup)
-    return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes,
-            "roofline": roofline("hbm", nbytes / (ms * 1e-3) / 1e9, "GB/s"),
+    timer = KernelTimer(steps)
+    ms = time_op(fn, steps, warmup, timer)
+    kms = timer.mean_ms()
+    return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes, "kernel_ms": kms,
+            "roofline": roofline("hbm", nbytes / (kms * 1e-3) / 1e9, "GB/s"),
             "config": {"workload": "ardq", "rows": R, "cols": H, "dtype": "bf16"}}
 
 
@@ -153,6 +156,52 @@ def bench_qmm(steps, warmup, dev):
     return {"ms": ms, "tops": ops / (ms * 1e-3) / 1e12, "gemm_kernel_ms": kms,
             "roofline": roofline("mfma", ops / (kms * 1e-3) / 1e12, "TFLOP/s"),
             "config": {"workload": "qmm", "M": M, "K": K, "N": N}}
+
+
+def _hbm_entry(fn, nbytes, steps, warmup, config):
+    """value: algorithmic bytes / wall time of the whole op call (host wrapper included);
+    roofline: the same bytes / device time of the op's kernels (HIP events on its stream)."""
+    timer = KernelTimer(steps)
+    ms = time_op(fn, steps, warmup, timer)
+    kms = timer.mean_ms()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(ms, 4), "kernel_ms": round(kms, 4),
+            "bytes": int(nbytes), "roofline": roofline("hbm", nbytes / (kms * 1e-3) / 1e9, "GB/s"), "config": config}
+
+
+def bench_routing(steps, warmup, dev):
+    """The routing operators on either side of the experts; algorithmic bytes = every input byte read
+    once plus every output byte written once."""
+    res = {}
+    d = cfgs.make_gating(dev)
+    T, E = d["x"].shape
+    k = d["k"]
+    res["gating"] = _hbm_entry(lambda: cb.moe_gating_top_k_softmax(d["x"], None, k), T * E * 4 + T * k * 12,
+                               steps, warmup, {"workload": "moe_gating_top_k_softmax", "tokens": T, "experts": E,
+                                               "k": k, "dtype": "fp32"})
+    del d
+    d = cfgs.make_rerouting(dev)
+    A, H = d["tokens"].shape
+    n, e = d["counts"].shape
+    res["rerouting"] = _hbm_entry(lambda: cb.moe_re_routing(d["tokens"], d["counts"], d["scales"]),
+                                  2 * A * H + A * (4 + 4 + 4) + n * e * 4 + e * 4, steps, warmup,
+                                  {"workload": "moe_re_routing", "rows": A, "hidden": H, "ranks": n,
+                                   "local_experts": e, "dtype": "int8"})
+    del d
+    d = cfgs.make_finalize(dev)
+    RK, H = d["epr"].shape
+    R, K = d["scales"].shape
+    res["finalize"] = _hbm_entry(
+        lambda: cb.moe_finalize_routing(d["epr"], d["esdr"], d["skip1"], None, None, d["scales"], None, 0),
+        RK * H * 2 + R * H * 2 * 2 + RK * 4 + R * K * 4, steps, warmup,
+        {"workload": "moe_finalize_routing", "tokens": R, "k": K, "hidden": H, "dtype": "bf16"})
+    del d
+    d = cfgs.make_dqsq(dev)
+    M, N2 = d["x"].shape
+    res["dqsq"] = _hbm_entry(lambda: cb.dequant_swiglu_quant(d["x"], d["weight_scale"], d["activation_scale"]),
+                             M * N2 * 4 + N2 * 4 + M * 4 + M * (N2 // 2) + M * 4, steps, warmup,
+                             {"workload": "dequant_swiglu_quant", "rows": M, "cols": N2, "dtype": "int32"})
+    return res
 
 
 def bench_copy(steps, warmup, dev):
@@ -213,8 +262,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", default="prefill,decode,ardq,qmm",
-                    help="comma list of prefill, decode, ardq, qmm, copy")
+    ap.add_argument("--only", default="prefill,decode,ardq,qmm,routing",
+                    help="comma list of prefill, decode, ardq, qmm, routing, copy")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -249,11 +298,14 @@ def main():
     if "ardq" in only:
         a = bench_ardq(args.steps, args.warmup, dev)
         out["ardq"] = {"value": round(a["gbs"], 1), "unit": "GB/s", "ms_per_step": round(a["ms"], 4),
+                       "kernel_ms": round(a["kernel_ms"], 4),
                        "roofline": a["roofline"], "config": a["config"]}
     if "qmm" in only:
         q = bench_qmm(args.steps, args.warmup, dev)
         out["qmm"] = {"value": round(q["tops"], 2), "unit": "TOPS", "ms_per_step": round(q["ms"], 4),
                       "roofline": q["roofline"], "config": q["config"]}
+    if "routing" in only:
+        out["routing"] = bench_routing(args.steps, args.warmup, dev)
     if "copy" in only:
         c = bench_copy(args.steps, args.warmup, dev)
         out["copy"] = {"value": round(c["gbs"], 1), "unit": "GB/s", "ms_per_step": round(c["ms"], 4),

@@ -11,6 +11,15 @@
                 (numpy default_rng(0), one draw per token) = 2048 rows; same shapes and scales,
                 followed by the int8 down-projection [2048, 2048] x [256, 2048, 7168] -> bf16.
 
+Routing operators around the experts (a 16384-token prefill batch, top-8 of 256 experts, hidden 7168):
+    gating      MoeGatingTopKSoftmax: fp32 logits [16384, 256] ~ N(0,1), k = 8
+    rerouting   MoeReRouting: int8 tokens [131072, 7168] from 16 ranks x 16 local experts, counts from
+                a multinomial over U(0.5, 1.5) weights (numpy default_rng(0)), fp32 per-token scales
+    finalize    MoeFinalizeRouting: bf16 expert outputs [131072, 7168], a random permutation as
+                expanded_src_to_dst_row (drop_pad_mode 0), fp32 scales [16384, 8], bf16 skip1 [16384, 7168]
+    dqsq        DequantSwigluQuant: int32 x [131072, 4096] ~ U{-2^15..2^15}, weight_scale [4096],
+                activation_scale [131072]
+
 Group counts come from numpy (host, exact and portable).  Large tensors are drawn on the device with
 a seeded torch generator (one generator per tensor, seeds in listed order), so every run on the same
 software stack sees identical data; tests that need CPU copies of them copy slices back.
@@ -109,3 +118,31 @@ def make_gmsq_decode(device="cuda", seed=0, with_down=True):
         d["down_weight"] = rand_i8((E_DEFAULT, 2048, 7168), device, seed + 31)
         d["down_weight_scale"] = rand_uniform((E_DEFAULT, 7168), 0.001, 0.01, device, seed + 32)
     return d
+
+
+def make_gating(device="cuda", tokens=16384, experts=256, k=8, seed=0):
+    return {"x": rand_normal((tokens, experts), device, seed + 1), "k": k}
+
+
+def make_rerouting(device="cuda", rows=131072, hidden=7168, ranks=16, experts=16, seed=0):
+    rng = np.random.default_rng(seed)
+    w = rng.uniform(0.5, 1.5, ranks * experts)
+    counts = rng.multinomial(rows, w / w.sum()).reshape(ranks, experts).astype(np.int64)
+    return {"tokens": rand_i8((rows, hidden), device, seed + 1),
+            "counts": torch.from_numpy(counts).to(device=device, dtype=torch.int32),
+            "scales": rand_uniform((rows,), 0.005, 0.02, device, seed + 2)}
+
+
+def make_finalize(device="cuda", tokens=16384, k=8, hidden=7168, seed=0):
+    g = _gen(device, seed + 3)
+    return {"epr": rand_normal((tokens * k, hidden), device, seed + 1, torch.bfloat16),
+            "esdr": torch.randperm(tokens * k, device=device, generator=g).to(torch.int32),
+            "scales": rand_uniform((tokens, k), 0.0, 0.25, device, seed + 2),
+            "skip1": rand_normal((tokens, hidden), device, seed + 4, torch.bfloat16)}
+
+
+def make_dqsq(device="cuda", rows=131072, n2=4096, seed=0):
+    g = _gen(device, seed + 1)
+    return {"x": torch.randint(-(1 << 15), 1 << 15, (rows, n2), dtype=torch.int32, device=device, generator=g),
+            "weight_scale": rand_uniform((n2,), 1e-4, 1e-3, device, seed + 2),
+            "activation_scale": rand_uniform((rows,), 0.005, 0.02, device, seed + 3)}

@@ -68,4 +68,25 @@ inline int check_launch()
     return hipGetLastError() == hipSuccess ? CB_OK : CB_ERR_LAUNCH;
 }
 
+// Optional per-thread instrumentation: events recorded around the next main kernel launch of an
+// operator (set by cb_set_kernel_timing, consumed and cleared by that launch).
+struct KernelTiming {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+extern thread_local KernelTiming g_timing;
+
+struct TimedLaunch {
+    hipStream_t st;
+    KernelTiming t;
+    explicit TimedLaunch(hipStream_t s) : st(s), t(g_timing)
+    {
+        g_timing = KernelTiming();
+        if (t.start) (void)hipEventRecord(t.start, st);
+    }
+    ~TimedLaunch()
+    {
+        if (t.stop) (void)hipEventRecord(t.stop, st);
+    }
+};
+
 }  // namespace cb

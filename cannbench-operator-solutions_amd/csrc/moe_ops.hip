@@ -92,26 +92,7 @@ static constexpr bool kSkinnyPrefetch = CB_SKINNY_PREFETCH;
 static constexpr bool kUseLdsCore = CB_LDS_CORE;
 static constexpr int kLdsWM = CB_LDS_WM, kLdsWN = CB_LDS_WN, kLdsStages = CB_LDS_STAGES, kLdsBK = CB_LDS_BK;
 
-// Optional per-thread instrumentation: events recorded around the next main GEMM kernel launch
-// (set by cb_set_kernel_timing, consumed and cleared by that launch).
-struct KernelTiming {
-    hipEvent_t start = nullptr, stop = nullptr;
-};
-static thread_local KernelTiming g_timing;
-
-struct TimedLaunch {
-    hipStream_t st;
-    KernelTiming t;
-    explicit TimedLaunch(hipStream_t s) : st(s), t(g_timing)
-    {
-        g_timing = KernelTiming();
-        if (t.start) (void)hipEventRecord(t.start, st);
-    }
-    ~TimedLaunch()
-    {
-        if (t.stop) (void)hipEventRecord(t.stop, st);
-    }
-};
+thread_local KernelTiming g_timing;
 
 template <int EPI>
 static void launch_gemm(GemmArgs& a, const int64_t* gl, int64_t E, int64_t batch, bool fast, hipStream_t st)

@@ -351,6 +351,7 @@ extern "C" int cb_add_rms_norm_dynamic_quant(const void* x1, const void* x2, con
     RowPlan p = plan_row(row_len, al);
     const float invN = 1.0f / (float)row_len;
     hipStream_t st = (hipStream_t)stream;
+    TimedLaunch timed(st);
     auto a = (const uint16_t*)x1;
     auto b = (const uint16_t*)x2;
     auto g = (const uint16_t*)gamma;
@@ -375,6 +376,7 @@ extern "C" int cb_dynamic_quant(const void* x, int dtype, int64_t rows, int64_t 
     if (rows > 0x7fffffffLL) return CB_ERR_SHAPE;
     if (!x || !y || !scale) return CB_ERR_NULL_POINTER;
     hipStream_t st = (hipStream_t)stream;
+    TimedLaunch timed(st);
     if (row_len > 16384) {  // longer than a register-resident row slice
         if (dtype == CB_DT_BFLOAT16)
             hipLaunchKernelGGL(dq_long_kernel<true>, dim3((unsigned)rows), dim3(512), 0, st, (const uint16_t*)x, row_len, y, scale);

@@ -73,10 +73,11 @@ const char* cb_status_string(int status);
 const char* cb_version(void);
 
 /*
- * Instrumentation (no reference counterpart): the next grouped / dense GEMM kernel launched by
- * this thread through any entry point records hipEvent_t `start_event` before and `stop_event`
- * after its main GEMM kernel on the call's stream, so a caller can time that kernel alone.
- * The setting is consumed by that launch.  Either event may be NULL.
+ * Instrumentation (no reference counterpart): the next operator call made by this thread records
+ * hipEvent_t `start_event` before and `stop_event` after its main kernel on the call's stream (the
+ * GEMM kernel of the grouped / dense operators; all kernels of the row and routing operators), so a
+ * caller can time the device work alone.  The setting is consumed by that call.  Either event may
+ * be NULL.
  */
 void cb_set_kernel_timing(void* start_event, void* stop_event);
 
