@@ -12,10 +12,10 @@ Reference plugins mirrored (paths under operators/):
   grouped_matmul_swiglu_quant  groupedmatmulswigluquant/csrc/ops/grouped_matmul_swiglu_quant/op_plugin/gmsq_plugin.cpp:40-145
   quant_matmul                 quantmatmul/csrc/ops/quant_matmul/op_plugin/quant_matmul_plugin.cpp:48-267
   grouped_matmul_quant         (no reference op) group semantics of groupedmatmul/csrc/ops/grouped_matmul/op_plugin/grouped_matmul_plugin.cpp:42-185
-  moe_re_routing               moererouting/csrc/ops/moe_re_routing/op_plugin/moe_re_routing_plugin.cpp:33-160
-  moe_finalize_routing         moefinalizerouting/csrc/ops/moe_finalize_routing/op_plugin/moe_finalize_routing_plugin.cpp:31-215
-  dequant_swiglu_quant         dequantswigluquant/csrc/ops/dequant_swiglu_quant/op_plugin/dqsq_plugin.cpp:32-140
-  moe_gating_top_k_softmax     moegatingtopksoftmax/csrc/ops/moe_gating_top_k_softmax/op_plugin/moe_gating_plugin.cpp:28-115
+  moe_re_routing               moererouting/csrc/ops/moe_re_routing/op_plugin/moe_re_routing_plugin.cpp:33-161
+  moe_finalize_routing         moefinalizerouting/csrc/ops/moe_finalize_routing/op_plugin/moe_finalize_routing_plugin.cpp:31-230
+  dequant_swiglu_quant         dequantswigluquant/csrc/ops/dequant_swiglu_quant/op_plugin/dqsq_plugin.cpp:32-151
+  moe_gating_top_k_softmax     moegatingtopksoftmax/csrc/ops/moe_gating_top_k_softmax/op_plugin/moe_gating_plugin.cpp:28-118
 """
 import torch
 
