@@ -82,6 +82,33 @@ __device__ __forceinline__ float wave_max(float v)
     return v;
 }
 
+// Raw buffer resource over [base, base + bytes): a load at an offset >= bytes returns zeros and
+// touches no memory, so an absent operand (bytes = 0) needs no branch around its load.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ v4i row_load(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2 /* nt */);
+}
+
+// Stores at offsets >= the resource size are dropped.
+__device__ __forceinline__ void row_store(v4i v, __amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 2 /* nt */);
+}
+
+constexpr uint32_t kOffNone = 0x80000000u;  // an offset past every row resource
+
+__device__ __forceinline__ int64_t uniform64(int64_t v)
+{
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 // 4x4 byte transpose: r[i] byte c -> o[c] byte i (v_perm_b32 only).
 __device__ __forceinline__ void transpose4x4_b8(u32 r0, u32 r1, u32 r2, u32 r3, u32& o0, u32& o1,
                                                 u32& o2, u32& o3)

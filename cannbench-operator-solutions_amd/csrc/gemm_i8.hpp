@@ -198,7 +198,7 @@ __device__ __forceinline__ void set_comp(uint4& v, int i, u32 x)
 //   the lane holds 16 B operands, one per column, and MFMA j yields column (16 c + j).
 // ============================================================================================
 #ifndef CB_SKINNY_OCC
-#define CB_SKINNY_OCC 3
+#define CB_SKINNY_OCC 2
 #endif
 template <int EPI, bool PREFETCH>
 __global__ __launch_bounds__(256, PREFETCH ? 2 : CB_SKINNY_OCC) void skinny_kernel(const GemmArgs a)
@@ -241,17 +241,20 @@ __global__ __launch_bounds__(256, PREFETCH ? 2 : CB_SKINNY_OCC) void skinny_kern
 
         const int arow = mb + c;
         const bool arow_ok = arow < r1;
-        const int8_t* xr = a.x + b * a.x_bstride + (int64_t)(arow_ok ? arow : r0) * K;
+        // activation row of this lane through a buffer resource: rows past the group and k past K
+        // read as zeros without a branch, so the activation load joins its chunk's weight loads
+        const __amdgpu_buffer_rsrc_t xres =
+            make_rsrc(a.x + b * a.x_bstride + (int64_t)(arow_ok ? arow : r0) * K, arow_ok ? (uint32_t)K : 0u);
 
-        auto load_chunk = [&](int kc, uint4 (&R)[16]) {
+        // one chunk = the activation operand (first, so waiting for it never waits for weights
+        // issued later) and 16 weight rows
+        auto load_chunk = [&](int kc, uint4 (&R)[16], v4i& A) {
+            A = __builtin_amdgcn_raw_buffer_load_b128(xres, (uint32_t)(kc * 64 + q * 16), 0, 0);
             const uint32_t kofs = (uint32_t)(kc * 64) * (uint32_t)N;  // rows past K read as zeros
 #pragma unroll
             for (int i = 0; i < 16; ++i) R[i] = buf_load16(wres, lane_off + kofs + (uint32_t)i * (uint32_t)N);
         };
-        auto mma_chunk = [&](int kc, const uint4 (&R)[16]) {
-            const int64_t kb = (int64_t)kc * 64 + q * 16;
-            const uint4 A = (arow_ok && kb < K) ? *reinterpret_cast<const uint4*>(xr + kb) : zero4();
-            const v4i av = as_v4i(A);
+        auto mma_chunk = [&](const uint4 (&R)[16], const v4i av) {
             // column block cb: the 4 B operands of columns 4 cb .. 4 cb + 3, built from dword cb
             // of the 16 loaded rows, consumed right away to keep the live range short
 #pragma unroll
@@ -275,20 +278,27 @@ __global__ __launch_bounds__(256, PREFETCH ? 2 : CB_SKINNY_OCC) void skinny_kern
         };
 
         if constexpr (PREFETCH) {
+            // the next chunk of this wave is always issued (chunks past K read zeros and fetch
+            // nothing), so the loop has no branch between the loads and the MFMAs that would make
+            // the compiler drain every outstanding load
             uint4 R[16];
-            if (wave < nch) load_chunk(wave, R);
+            v4i A;
+            load_chunk(wave, R, A);
             for (int kc = wave; kc < nch; kc += 4) {
                 uint4 Rn[16];
-                if (kc + 4 < nch) load_chunk(kc + 4, Rn);
-                mma_chunk(kc, R);
+                v4i An;
+                load_chunk(kc + 4, Rn, An);
+                mma_chunk(R, A);
 #pragma unroll
                 for (int i = 0; i < 16; ++i) R[i] = Rn[i];
+                A = An;
             }
         } else {
             for (int kc = wave; kc < nch; kc += 4) {
                 uint4 R[16];
-                load_chunk(kc, R);
-                mma_chunk(kc, R);
+                v4i A;
+                load_chunk(kc, R, A);
+                mma_chunk(R, A);
             }
         }
 

@@ -109,22 +109,59 @@ __global__ __launch_bounds__(512) void ardq_kernel(const uint16_t* __restrict__ 
     const int nvec = (int)(n / VEC);
     float z[NV][VEC];
     float ss = 0.0f, mz = 0.0f;
+    if constexpr (VEC == 8) {
+        // 16-byte rows through buffer resources: every load of the thread's slice is issued up
+        // front with no branch (lanes past the row read zeros, which add nothing to the sums, and
+        // their stores are dropped), so the whole slice is in flight at once
+        const uint32_t rb = (uint32_t)(n * 2);
+        const auto r1 = row_rsrc(x1 + base, rb), r2 = row_rsrc(x2 + base, rb), rg = row_rsrc(gamma, rb);
+        const auto ro = row_rsrc(xout + base, rb);
+        uint32_t off[NV];
+        v4i A[NV], B[NV], G[NV];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int v = i * blockDim.x + threadIdx.x;
-        if (v < nvec) {
-            const int64_t e = base + (int64_t)v * VEC;
-            Vec16<VEC> a = ldv<VEC>(x1 + e), b = ldv<VEC>(x2 + e), g = ldv<VEC>(gamma + (int64_t)v * VEC);
-            Vec16<VEC> o;
+        for (int i = 0; i < NV; ++i) {
+            const int v = i * blockDim.x + threadIdx.x;
+            off[i] = v < nvec ? (uint32_t)v * 16u : kOffNone;
+            A[i] = row_load(r1, off[i]);
+            B[i] = row_load(r2, off[i]);
+            G[i] = __builtin_amdgcn_raw_buffer_load_b128(rg, off[i], 0, 0);  // gamma is shared by all rows
+        }
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) {
-                const float xf = ld16<BF16>(a.v[j]) + ld16<BF16>(b.v[j]);
-                o.v[j] = st16<BF16>(xf);
+        for (int i = 0; i < NV; ++i) {
+            const uint16_t* a = reinterpret_cast<const uint16_t*>(&A[i]);
+            const uint16_t* b = reinterpret_cast<const uint16_t*>(&B[i]);
+            const uint16_t* g = reinterpret_cast<const uint16_t*>(&G[i]);
+            uint16_t o[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float xf = ld16<BF16>(a[j]) + ld16<BF16>(b[j]);
+                o[j] = st16<BF16>(xf);
                 ss += xf * xf;
-                z[i][j] = xf * ld16<BF16>(g.v[j]);
+                z[i][j] = xf * ld16<BF16>(g[j]);
                 mz = fmaxf(mz, fabsf(z[i][j]));
             }
-            stv<VEC>(xout + e, o);
+            v4i ov;
+            __builtin_memcpy(&ov, o, 16);
+            row_store(ov, ro, off[i]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int v = i * blockDim.x + threadIdx.x;
+            if (v < nvec) {
+                const int64_t e = base + (int64_t)v * VEC;
+                Vec16<VEC> a = ldv<VEC>(x1 + e), b = ldv<VEC>(x2 + e), g = ldv<VEC>(gamma + (int64_t)v * VEC);
+                Vec16<VEC> o;
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) {
+                    const float xf = ld16<BF16>(a.v[j]) + ld16<BF16>(b.v[j]);
+                    o.v[j] = st16<BF16>(xf);
+                    ss += xf * xf;
+                    z[i][j] = xf * ld16<BF16>(g.v[j]);
+                    mz = fmaxf(mz, fabsf(z[i][j]));
+                }
+                stv<VEC>(xout + e, o);
+            }
         }
     }
     block_sum_max(ss, mz, red);
@@ -135,14 +172,30 @@ __global__ __launch_bounds__(512) void ardq_kernel(const uint16_t* __restrict__ 
     const float sc = sm * kInv127;
     const float k = rstd / sc;
     if (threadIdx.x == 0) scale[row] = sc;
+    if constexpr (VEC == 8) {
+        const auto ry = row_rsrc(y + base, (uint32_t)n);
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int v = i * blockDim.x + threadIdx.x;
-        if (v < nvec) {
-            int q[VEC];
+        for (int i = 0; i < NV; ++i) {
+            const int v = i * blockDim.x + threadIdx.x;
+            int q[8];
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) q[j] = rint16(z[i][j] * k);
-            sty8<VEC>(y + base + (int64_t)v * VEC, q);
+            for (int j = 0; j < 8; ++j) q[j] = rint16(z[i][j] * k);
+            typedef int rv2i __attribute__((ext_vector_type(2)));
+            rv2i w;
+            w[0] = (int)pack4_i8(q[0], q[1], q[2], q[3]);
+            w[1] = (int)pack4_i8(q[4], q[5], q[6], q[7]);
+            __builtin_amdgcn_raw_buffer_store_b64(w, ry, v < nvec ? (uint32_t)v * 8u : kOffNone, 0, 2);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int v = i * blockDim.x + threadIdx.x;
+            if (v < nvec) {
+                int q[VEC];
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) q[j] = rint16(z[i][j] * k);
+                sty8<VEC>(y + base + (int64_t)v * VEC, q);
+            }
         }
     }
 }
@@ -157,15 +210,35 @@ __global__ __launch_bounds__(512) void dq_kernel(const uint16_t* __restrict__ x,
     const int nvec = (int)(n / VEC);
     float xv[NV][VEC];
     float s = 0.0f, a = 0.0f;
+    if constexpr (VEC == 8) {
+        // branch-free 16-byte buffer loads of the whole slice (zeros past the row)
+        const auto rx = row_rsrc(x + base, (uint32_t)(n * 2));
+        v4i X[NV];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int v = i * blockDim.x + threadIdx.x;
-        if (v < nvec) {
-            Vec16<VEC> t = ldv<VEC>(x + base + (int64_t)v * VEC);
+        for (int i = 0; i < NV; ++i) {
+            const int v = i * blockDim.x + threadIdx.x;
+            X[i] = row_load(rx, v < nvec ? (uint32_t)v * 16u : kOffNone);
+        }
 #pragma unroll
-            for (int j = 0; j < VEC; ++j) {
-                xv[i][j] = ld16<BF16>(t.v[j]);
+        for (int i = 0; i < NV; ++i) {
+            const uint16_t* t = reinterpret_cast<const uint16_t*>(&X[i]);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                xv[i][j] = ld16<BF16>(t[j]);
                 a = fmaxf(a, fabsf(xv[i][j]));
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int v = i * blockDim.x + threadIdx.x;
+            if (v < nvec) {
+                Vec16<VEC> t = ldv<VEC>(x + base + (int64_t)v * VEC);
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) {
+                    xv[i][j] = ld16<BF16>(t.v[j]);
+                    a = fmaxf(a, fabsf(xv[i][j]));
+                }
             }
         }
     }
