@@ -142,8 +142,9 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
         const int cid = (i * NW + wave) * 64 + lane;  // 16-byte chunk id in the A tile
         const int row = cid / ACH, pos = cid % ACH;
         const int q = pos ^ a_swz(row);
-        const int rr = row < vrows ? row : vrows - 1;
-        a_off[i] = (uint32_t)rr * (uint32_t)K + (uint32_t)(q * 16);
+        // rows past the tile's valid rows point past the resource: they read zeros and fetch
+        // nothing, so a partial tile moves only its valid rows
+        a_off[i] = row < vrows ? (uint32_t)row * (uint32_t)K + (uint32_t)(q * 16) : 0x80000000u;
     }
     uint32_t b_off[C::B_ISSUE];
 #pragma unroll
