@@ -314,6 +314,9 @@ def main():
         out["roofline"]["traffic"] = traffic_from_profiles("prefill_gemm")
     if "decode" in out:
         out["decode"]["roofline"]["traffic"] = traffic_from_profiles("decode_gemm")
+    for name in ("finalize", "rerouting", "dqsq"):
+        if name in out.get("routing", {}):
+            out["routing"][name]["roofline"]["traffic"] = traffic_from_profiles("routing_" + name)
     if not args.no_cpu and "prefill" in keep:
         out["cpu_baseline"] = cpu_baseline(keep["prefill"])
     print(json.dumps(out), flush=True)
