@@ -220,3 +220,43 @@ def test_routing_torch_ops(cb):
     assert outs[2].cpu().tolist() == [0, 3, 4, 1, 2, 5]
     out = torch.ops.cann_bench.moe_finalize_routing(tok, torch.arange(6, dtype=torch.int32, device=DEV))
     torch.testing.assert_close(out, tok, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("case", ["odd_h", "big_k", "misaligned"])
+def test_moe_finalize_routing_scalar_paths(cb, orc, case):
+    """Shapes off the 16-byte vector path: odd H, K above the LDS slot table, and rows that are
+    not 16-byte aligned (a view one element into a larger buffer)."""
+    g = gen({"odd_h": 1, "big_k": 2, "misaligned": 3}[case])
+    R, K, H = (9, 3, 37) if case == "odd_h" else ((6, 80, 64) if case == "big_k" else (7, 4, 64))
+    num_dst = R * K
+    base = torch.randn(num_dst * H + 1, generator=g).to(torch.bfloat16)
+    epr = base[1:].reshape(num_dst, H) if case == "misaligned" else base[:num_dst * H].reshape(num_dst, H)
+    esdr = torch.randperm(num_dst, generator=g).to(torch.int32)
+    esdr[0] = -1
+    scales = torch.rand(R, K, generator=g)
+    skip = torch.randn(R, H, generator=g).to(torch.bfloat16)
+    bias = torch.randn(5, H, generator=g).to(torch.bfloat16)
+    expert = torch.randint(0, 5, (R, K), generator=g).to(torch.int32)
+    dev_base = base.to(DEV)
+    depr = dev_base[1:].reshape(num_dst, H) if case == "misaligned" else dev_base[:num_dst * H].reshape(num_dst, H)
+    out = cb.moe_finalize_routing(depr, esdr.to(DEV), skip.to(DEV), None, bias.to(DEV), scales.to(DEV),
+                                  expert.to(DEV), 2)
+    torch.cuda.synchronize()
+    want = orc.moe_finalize_routing(bits16(epr), "bf16", esdr.numpy(), K, bits16(skip), None, bits16(bias),
+                                    scales.numpy(), "f32", expert.numpy(), 2)
+    np.testing.assert_array_equal(bits16(out), want)
+
+
+def test_moe_re_routing_large_cell_table(cb, orc):
+    """More than 8192 (rank, expert) cells: the serial prefix kernel."""
+    g = gen(11)
+    n, e, H = 40, 256, 32
+    cnt = torch.randint(0, 2, (n, e), generator=g)
+    total = int(cnt.sum())
+    tokens = torch.randn(total, H, generator=g).to(torch.bfloat16)
+    pt, ps, pi, etn = cb.moe_re_routing(tokens.to(DEV), cnt.to(torch.int64).to(DEV))
+    torch.cuda.synchronize()
+    r_out, _, r_idx, r_etn, _ = orc.moe_re_routing(bits16(tokens), cnt.numpy())
+    np.testing.assert_array_equal(etn.cpu().numpy(), r_etn)
+    np.testing.assert_array_equal(pi.cpu().numpy(), r_idx)
+    np.testing.assert_array_equal(bits16(pt), r_out)
