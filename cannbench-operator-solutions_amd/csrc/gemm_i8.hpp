@@ -26,7 +26,9 @@
 
 namespace cb {
 
-enum { EPI_SWIGLU = 0, EPI_DEQUANT = 1, EPI_I32 = 2 };
+// EPI_SWIGLU_Q: SwiGLU with the per-token requant fused (persistent prefill kernel; the fp32
+// activation stays on chip)
+enum { EPI_SWIGLU = 0, EPI_DEQUANT = 1, EPI_I32 = 2, EPI_SWIGLU_Q = 3 };
 
 enum { BIAS_NONE = 0, BIAS_I32 = 1, BIAS_F16 = 2, BIAS_BF16 = 3, BIAS_F32 = 4 };
 
@@ -66,6 +68,11 @@ struct EpiArgs {
     float* act;
     u32* amax;
     int64_t H;
+    // fused requant (EPI_SWIGLU_Q)
+    u32* arrive;       // per row tile: column tiles that have published their row maxima
+    u32* status;       // set to 1 if a row tile's exchange timed out
+    int8_t* yq;        // int8 output [M, H]
+    float* yq_scale;   // fp32 row scales [M]
 };
 
 struct GemmArgs {

@@ -26,6 +26,10 @@ typedef int v2i __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 #define CB_LDS __attribute__((address_space(3)))
 
+// Polls of a row tile's arrival counter before the fused requant gives up (each poll sleeps about
+// 512 cycles plus an atomic round trip: a few hundred ms in total, against microseconds normally).
+constexpr int kExchangeSpinLimit = 1 << 16;
+
 // The LDS DMA and the stage barrier are written as inline asm on purpose: when the compiler sees
 // buffer_load ... lds it must assume every later LDS read may alias the DMA target and waits for
 // vmcnt(0), and a __syncthreads() fence also drains vmcnt - either would serialise the stage
@@ -84,44 +88,25 @@ struct LdsCfg {
     static_assert(FN >= 2 && FN % 2 == 0, "wave tile must hold gate/up pairs");
 };
 
+// One 256 x 256 output tile (row tile mt, column tile nt, batch b).  Called once per workgroup by
+// lds_gemm_kernel and in a loop by the persistent fused-requant kernel.
 template <int EPI, int WM, int WN, int STAGES, int BKT>
-__global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArgs a)
+__device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, const int nt, const int64_t b,
+                                              uint8_t* smem, const int arr_idx = 0, const u32 arr_target = 0)
 {
     using C = LdsCfg<WM, WN, STAGES, BKT>;
+    constexpr bool SW = EPI == EPI_SWIGLU || EPI == EPI_SWIGLU_Q;
     constexpr int KS = C::KS, ACH = C::ACH;
     // A swizzle key: spreads the 16 rows of a ds_read_b128 phase over all 64 banks
     // (BK 64: 4 rows per 256 bytes, key (r >> 2) & 3; BK 128: 2 rows per 256 bytes, key (r >> 1) & 7)
     auto a_swz = [](int r) { return ACH == 4 ? ((r >> 2) & 3) : ((r >> 1) & 7); };
     constexpr int BM = C::BM, BN = C::BN, BK = C::BK, NW = C::NW, TN = C::TN, FM = C::FM,
                   FN = C::FN;
-    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
     const int64_t K = a.K, N = a.N;
     const EpiArgs& e = a.epi;
-    const int64_t b = blockIdx.y;
-
-    // ---- tile selection (XCD remap + GROUP_M swizzle) -------------------------------------
-    // Measured on the prefill and dense shapes: the plain dispatch order (workgroups round-robin
-    // over the XCDs) is as good as or better than an XCD-contiguous remap of the tile order.
-#ifdef CB_XCD_REMAP
-    const int pid = xcd_remap(blockIdx.x, gridDim.x);
-#else
-    const int pid = blockIdx.x;
-#endif
-#ifndef CB_GROUP_M
-#define CB_GROUP_M 4
-#endif
-    constexpr int GROUP_M = CB_GROUP_M;
-    const int T_m = a.gt.total_mtiles, T_n = a.ntiles;
-    const int per_group = GROUP_M * T_n;
-    const int gid = pid / per_group;
-    const int first_m = gid * GROUP_M;
-    const int gsz = (T_m - first_m) < GROUP_M ? (T_m - first_m) : GROUP_M;
-    const int mt = first_m + (pid % per_group) % gsz;
-    const int nt = (pid % per_group) / gsz;
 
     const int g = group_of_tile(a.gt, mt);
     const int rs = g ? a.gt.row_end[g - 1] : 0;
@@ -154,7 +139,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
         const int c = pos ^ ((row & 7) << 1);  // logical 16-column chunk
         int64_t col;
         bool ok;
-        if constexpr (EPI == EPI_SWIGLU) {
+        if constexpr (SW) {
             const int64_t j = (int64_t)nt * (BN / 2) + 16 * (c & 7);
             ok = j < e.H;
             col = c < 8 ? j : e.H + j;
@@ -181,7 +166,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
     };
 
     auto tcol = [&](int fn) -> int {  // first tile column of wave fragment fn
-        if constexpr (EPI == EPI_SWIGLU)
+        if constexpr (SW)
             return fn < FN / 2 ? wn * (TN / 2) + fn * 32 : BN / 2 + wn * (TN / 2) + (fn - FN / 2) * 32;
         else
             return wn * TN + fn * 32;
@@ -369,7 +354,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
 #endif
     // ---- epilogue.  32x32 C layout: lane l holds column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4
     const int lr = (lane >> 5) * 4;
-    if constexpr (EPI == EPI_SWIGLU) {
+    if constexpr (SW) {
         // act tile [256 rows][128 act columns] fp32 staged in LDS, then written with 16-byte stores
         // and one row-max atomic per (row, tile)
         const int64_t H = e.H;
@@ -406,22 +391,86 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
         const int lrow = tid / TPR, part = tid % TPR;
         const int row = m0 + lrow;
         const int64_t j0 = (int64_t)nt * (BN / 2) + part * CPT;
+        const CB_LDS v4f* src = (const CB_LDS v4f*)(st + lrow * C::EPI_PITCH + part * CPT * 4);
         float m = 0.0f;
-        if (row < r1) {
-            const CB_LDS v4f* src = (const CB_LDS v4f*)(st + lrow * C::EPI_PITCH + part * CPT * 4);
-            v4f* dst = reinterpret_cast<v4f*>(e.act + (int64_t)row * H + j0);
+        if constexpr (EPI == EPI_SWIGLU) {
+            if (row < r1) {
+                v4f* dst = reinterpret_cast<v4f*>(e.act + (int64_t)row * H + j0);
+#pragma unroll
+                for (int i = 0; i < CPT / 4; ++i) {
+                    if (j0 + 4 * i < H) {
+                        const v4f v = src[i];
+                        dst[i] = v;
+                        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+                    }
+                }
+            }
+#pragma unroll
+            for (int o = 1; o < TPR; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            if (part == 0 && row < r1) atomicMax(e.amax + row, __float_as_uint(m));
+        } else {
+            // Fused requant.  The thread keeps its 64 act values in registers; the row maxima of the
+            // ntiles column tiles of this row tile (all resident at once in the persistent grid) are
+            // combined with device-scope atomics, and each tile quantises its own slice once every
+            // workgroup of its exchange group (arr_target of them, counted at arrive[arr_idx]) has
+            // published.  The fp32 activation never leaves the CU.
+            v4f v[CPT / 4];
 #pragma unroll
             for (int i = 0; i < CPT / 4; ++i) {
-                if (j0 + 4 * i < H) {
-                    const v4f v = src[i];
-                    dst[i] = v;
-                    m = fmaxf(m, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+                v[i] = src[i];
+                if (row < r1 && j0 + 4 * i < H)
+                    m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i][0]), fabsf(v[i][1])), fmaxf(fabsf(v[i][2]), fabsf(v[i][3]))));
+            }
+#pragma unroll
+            for (int o = 1; o < TPR; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            // Every shared word of the exchange (row maxima, arrival counts) is touched only by
+            // agent-scope atomics, which are coherent across the XCDs without flushing or
+            // invalidating L2 (a __threadfence() here would invalidate the GEMM's cached slabs).
+            // Ordering: each maximum has completed (vmcnt 0) before the barrier, and the arrival
+            // count is bumped after it.
+            if (part == 0 && row < r1)
+                __hip_atomic_fetch_max(e.amax + row, __float_as_uint(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (tid == 0) {
+                __hip_atomic_fetch_add(e.arrive + arr_idx, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                // bounded wait: every wave reaches the end even if a column tile never arrives (the
+                // status word then reports the failure and the tile quantises with what it has)
+                int spins = 0;
+                while (__hip_atomic_load(e.arrive + arr_idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < arr_target) {
+                    __builtin_amdgcn_s_sleep(8);
+                    if (++spins > kExchangeSpinLimit) {
+                        __hip_atomic_fetch_or(e.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        break;
+                    }
+                }
+            }
+            __syncthreads();
+            if (row < r1) {
+                // the final row maximum (an agent-scope atomic load sees every tile's update)
+                float am = __uint_as_float(
+                    __hip_atomic_load(e.amax + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+                if (!(am > kFltMin)) am = kFltMin;
+                const float inv = 127.0f / am;
+                if (nt == 0 && part == 0) e.yq_scale[row] = am * kInv127;
+                int8_t* dst = e.yq + (int64_t)row * H + j0;
+#pragma unroll
+                for (int c = 0; c < CPT / 16; ++c) {
+                    if (j0 + 16 * c < H) {
+                        v4i w;
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const v4f t = v[4 * c + q];
+                            // clamp then narrow == saturating rint16; an all-zero row gives 0 * inf =
+                            // NaN, which rint16 maps to 0 (the standalone requant's rule)
+                            w[q] = (int)pack4_i8(rint16(t[0] * inv), rint16(t[1] * inv), rint16(t[2] * inv),
+                                                 rint16(t[3] * inv));
+                        }
+                        *reinterpret_cast<v4i*>(dst + 16 * c) = w;
+                    }
                 }
             }
         }
-#pragma unroll
-        for (int o = 1; o < TPR; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        if (part == 0 && row < r1) atomicMax(e.amax + row, __float_as_uint(m));
     } else if constexpr (EPI == EPI_I32) {
         int32_t* ob = (int32_t*)e.out + b * e.out_bstride;
 #pragma unroll
@@ -478,6 +527,77 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
                 *reinterpret_cast<v4i*>(ob + (int64_t)row * N + col) =
                     *(const CB_LDS v4i*)(st + lrow * C::EPI_PITCH + ch * 16);
         }
+    }
+}
+
+// Non-persistent launch: one tile per workgroup.
+template <int EPI, int WM, int WN, int STAGES, int BKT>
+__global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArgs a)
+{
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    // ---- tile selection (GROUP_M swizzle) ---------------------------------------------------
+    // Measured on the prefill and dense shapes: the plain dispatch order (workgroups round-robin
+    // over the XCDs) is as good as or better than an XCD-contiguous remap of the tile order.
+#ifdef CB_XCD_REMAP
+    const int pid = xcd_remap(blockIdx.x, gridDim.x);
+#else
+    const int pid = blockIdx.x;
+#endif
+#ifndef CB_GROUP_M
+#define CB_GROUP_M 4
+#endif
+    constexpr int GROUP_M = CB_GROUP_M;
+    const int T_m = a.gt.total_mtiles, T_n = a.ntiles;
+    const int per_group = GROUP_M * T_n;
+    const int gid = pid / per_group;
+    const int first_m = gid * GROUP_M;
+    const int gsz = (T_m - first_m) < GROUP_M ? (T_m - first_m) : GROUP_M;
+    const int mt = first_m + (pid % per_group) % gsz;
+    const int nt = (pid % per_group) / gsz;
+    lds_gemm_tile<EPI, WM, WN, STAGES, BKT>(a, mt, nt, blockIdx.y, smem);
+}
+
+// Persistent GroupedMatmulSwigluQuant with the requant fused.  gridDim.x workgroups, at most one per
+// CU, all resident together.  A slot is RT consecutive row tiles x ntiles column tiles; its
+// workgroups compute round r's row tiles (slot + slots * r) * RT .. + RT - 1 and meet once per round
+// at the row-max exchange, which keeps the RT row tiles of the slot in step through K.  With 16
+// column tiles on 256 CUs (RT = 4, 4 slots) workgroup b (dispatched to XCD b % 8) gets slot
+// (b % 8) / 2: each XCD holds 4 row tiles x the same 8 column tiles, the GROUP_M = 4 footprint of
+// the non-persistent kernel, and the 8 workgroups sharing an activation slab sit on one XCD.
+template <int WM, int WN, int STAGES, int BKT>
+__global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_swiglu_q_kernel(const GemmArgs a)
+{
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    const int ntl = a.ntiles;
+    int slot, rt, nt, slots, RT;
+    if (ntl == 16 && gridDim.x == 256) {
+        // measured: this round-robin-aware assignment beats a contiguous one (blocks 64 s .. 64 s + 63
+        // per slot) by 20%, which confirms the round-robin dispatch over the XCDs
+        const int x = blockIdx.x & 7, j = blockIdx.x >> 3;
+        slot = x >> 1;
+        rt = j >> 3;
+        nt = (x & 1) * 8 + (j & 7);
+        slots = 4;
+        RT = 4;
+    } else {
+        slot = blockIdx.x / ntl;
+        rt = 0;
+        nt = blockIdx.x % ntl;
+        slots = (int)gridDim.x / ntl;
+        RT = 1;
+    }
+    const u32 target = (u32)(RT * ntl);
+    for (int q = slot; q * RT < a.gt.total_mtiles; q += slots) {
+        const int mt = q * RT + rt;
+        if (mt < a.gt.total_mtiles) {
+            lds_gemm_tile<EPI_SWIGLU_Q, WM, WN, STAGES, BKT>(a, mt, nt, 0, smem, q, target);
+        } else {
+            // past the last row tile in the final round: still take part in the exchange so the
+            // slot's other row tiles see every arrival
+            if (threadIdx.x == 0)
+                __hip_atomic_fetch_add(a.epi.arrive + q, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();  // the next tile's DMAs overwrite the LDS this epilogue just read
     }
 }
 

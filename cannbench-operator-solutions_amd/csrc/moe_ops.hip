@@ -53,19 +53,39 @@ static void fill_u32(u32* p, int64_t n, u32 v, hipStream_t st)
 
 static inline int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
-// Workspace layout of GroupedMatmulSwigluQuant: fp32 activation [M, H] then u32 row abs-max [M].
+// Workspace layout of GroupedMatmulSwigluQuant: u32 row abs-max [M], u32 arrival counters (one per
+// 256-row tile; at most M / 256 + E tiles), a u32 status word, then the fp32 activation [M, H] that
+// only the non-persistent paths (decode-shaped groups, unaligned shapes) write.
 struct GmsqWorkspace {
-    int64_t act_off, amax_off, total;
+    int64_t amax_off, arrive_off, status_off, act_off, total, n_arrive;
 };
 
-static GmsqWorkspace gmsq_workspace(int64_t M, int64_t N)
+static GmsqWorkspace gmsq_workspace(int64_t M, int64_t N, int64_t E)
 {
     GmsqWorkspace w;
     const int64_t H = N / 2;
-    w.act_off = 0;
-    w.amax_off = round_up(M * H * 4, 256);
-    w.total = w.amax_off + round_up(M * 4, 256);
+    w.n_arrive = M / 256 + E + 1;
+    w.amax_off = 0;
+    w.arrive_off = round_up(M * 4, 256);
+    w.status_off = w.arrive_off + round_up(w.n_arrive * 4, 256);
+    w.act_off = w.status_off + 256;
+    w.total = w.act_off + round_up(M * H * 4, 256);
     return w;
+}
+
+// Compute units of the current device (cached per device): the persistent fused kernel keeps one
+// workgroup per CU.
+static int device_cus()
+{
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (cus[dev] == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) v = -1;
+        cus[dev] = v;
+    }
+    return cus[dev];
 }
 
 static constexpr int kSkinnyMaxRows = 32;  // groups up to this many rows take the skinny core
@@ -89,7 +109,11 @@ static constexpr bool kSkinnyPrefetch = CB_SKINNY_PREFETCH;
 #ifndef CB_LDS_BK
 #define CB_LDS_BK 64
 #endif
+#ifndef CB_FUSED_REQUANT
+#define CB_FUSED_REQUANT 1
+#endif
 static constexpr bool kUseLdsCore = CB_LDS_CORE;
+static constexpr bool kFusedRequant = CB_FUSED_REQUANT;
 static constexpr int kLdsWM = CB_LDS_WM, kLdsWN = CB_LDS_WN, kLdsStages = CB_LDS_STAGES, kLdsBK = CB_LDS_BK;
 
 thread_local KernelTiming g_timing;
@@ -176,7 +200,7 @@ extern "C" int64_t cb_grouped_matmul_swiglu_quant_workspace_size(int64_t M, int6
     (void)K;
     (void)E;
     if (M <= 0 || N <= 0) return 0;
-    return gmsq_workspace(M, N).total;
+    return gmsq_workspace(M, N, E).total;
 }
 
 extern "C" int cb_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* weight, const float* weight_scale,
@@ -192,7 +216,7 @@ extern "C" int cb_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* wei
     if (M > 0x7fffffffLL) return CB_ERR_SHAPE;
     const int vs = validate_group_list(group_list, group_len, E, M);
     if (vs != CB_OK) return vs;
-    const GmsqWorkspace ws = gmsq_workspace(M, N);
+    const GmsqWorkspace ws = gmsq_workspace(M, N, E);
     if (!workspace || workspace_bytes < ws.total) return CB_ERR_WORKSPACE;
 
     hipStream_t st = (hipStream_t)stream;
@@ -200,6 +224,8 @@ extern "C" int cb_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* wei
     uint8_t* wsb = (uint8_t*)workspace;
     float* act = (float*)(wsb + ws.act_off);
     u32* amax = (u32*)(wsb + ws.amax_off);
+    u32* arrive = (u32*)(wsb + ws.arrive_off);
+    u32* status = (u32*)(wsb + ws.status_off);
 
     GemmArgs a;
     std::memset(&a, 0, sizeof(a));
@@ -215,8 +241,35 @@ extern "C" int cb_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* wei
     a.epi.amax = amax;
     a.epi.H = H;
 
+    a.epi.arrive = arrive;
+    a.epi.status = status;
+    a.epi.yq = y;
+    a.epi.yq_scale = y_scale;
+
     const bool fast = K > 0 && K % 16 == 0 && H % 16 == 0 && aligned(x, 16) && aligned(weight, 16) &&
                       aligned(act, 16) && aligned(weight_scale, 4);
+    if (fast && kUseLdsCore && kFusedRequant) {
+        // persistent GEMM with the requant fused: every column tile of a row tile is resident at once
+        build_group_table(a.gt, group_list, E, 256);
+        const int ntl = (int)((H + 127) / 128);
+        const int cus = device_cus();
+        if (a.gt.max_rows > kSkinnyMaxRows && cus >= ntl && a.gt.total_mtiles <= ws.n_arrive && aligned(y, 16)) {
+            const int slots = (ntl == 16 && cus >= 256) ? 16 : cus / ntl;  // 256 workgroups for 16 column tiles
+            a.ntiles = ntl;
+            // amax, arrival counters and the status word are contiguous: one fill clears them
+            fill_u32(amax, (ws.status_off - ws.amax_off) / 4 + 1, 0u, st);
+            using Cfg = LdsCfg<kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
+            auto kern = lds_gemm_swiglu_q_kernel<kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
+            static bool attr_set = false;  // idempotent, so a benign race
+            if (!attr_set) {
+                (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS_BYTES);
+                attr_set = true;
+            }
+            TimedLaunch timed(st);
+            hipLaunchKernelGGL(kern, dim3((unsigned)(slots * ntl)), dim3(Cfg::NT), Cfg::LDS_BYTES, st, a);
+            return check_launch();
+        }
+    }
     fill_u32(amax, M, 0u, st);
     launch_gemm<EPI_SWIGLU>(a, group_list, E, 1, fast, st);
     hipLaunchKernelGGL(gmsq_requant_kernel, dim3((unsigned)M), dim3(256), 0, st, act, amax, H, y, y_scale);

@@ -173,6 +173,18 @@ def test_gmsq_zero_rows(cb):
     assert (ys[2:4].cpu().numpy() == fm).all()
 
 
+def test_gmsq_zero_rows_fused(cb):
+    """All-zero rows inside groups large enough for the persistent fused-requant GEMM."""
+    x, w, ws, xs, gl = _gmsq_inputs([70, 300], 512, 1024, 3)
+    x[10:12] = 0
+    x[200] = 0
+    y, ys = cb.grouped_matmul_swiglu_quant(x, w, ws, xs, gl)
+    fm = np.float32(1.1754944e-38) * np.float32(1 / 127)
+    for r in (10, 11, 200):
+        assert (y[r] == 0).all()
+        assert ys[r].item() == fm
+
+
 def test_gmsq_repeatable_and_stream_ordered(cb):
     """Two back-to-back calls on a side stream give identical results (the workspace's row-max
     buffer is re-cleared on every call)."""
