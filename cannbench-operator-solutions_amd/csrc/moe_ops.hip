@@ -104,10 +104,10 @@ static constexpr bool kSkinnyPrefetch = CB_SKINNY_PREFETCH;
 #define CB_LDS_WN 2
 #endif
 #ifndef CB_LDS_STAGES
-#define CB_LDS_STAGES 4
+#define CB_LDS_STAGES 2
 #endif
 #ifndef CB_LDS_BK
-#define CB_LDS_BK 64
+#define CB_LDS_BK 128
 #endif
 #ifndef CB_FUSED_REQUANT
 #define CB_FUSED_REQUANT 1
