@@ -290,6 +290,9 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
 #ifdef CB_PROFILE
         uint64_t prof_acc[4] = {0, 0, 0, 0};
         CB_PROF_T(tstart);
+#ifdef CB_PROFILE
+        const uint64_t rstart = __builtin_amdgcn_s_memrealtime();
+#endif
 #endif
         wait_vmcnt_barrier<(STAGES - 1) * C::ISSUE>();
         load(0, 0, a0, b0);
@@ -325,6 +328,12 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
             atomicAdd(&cb_prof[1], prof_acc[1]);
             atomicAdd(&cb_prof[2], prof_acc[2]);
             atomicAdd(&cb_prof[3], 1ull);
+            // the shader clock follows from memtime (core clock) over memrealtime (100 MHz)
+            atomicAdd(&cb_prof[4], __builtin_amdgcn_s_memrealtime() - rstart);
+            if (vrows < BM) {
+                atomicAdd(&cb_prof[5], prof_acc[2]);
+                atomicAdd(&cb_prof[6], 1ull);
+            }
         }
 #endif
     };
@@ -437,6 +446,9 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
                 // bounded wait: every wave reaches the end even if a column tile never arrives (the
                 // status word then reports the failure and the tile quantises with what it has)
                 int spins = 0;
+#ifdef CB_PROFILE
+                const uint64_t tx0 = __builtin_amdgcn_s_memtime();
+#endif
                 while (__hip_atomic_load(e.arrive + arr_idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < arr_target) {
                     __builtin_amdgcn_s_sleep(8);
                     if (++spins > kExchangeSpinLimit) {
@@ -444,6 +456,9 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
                         break;
                     }
                 }
+#ifdef CB_PROFILE
+                atomicAdd(&cb_prof[7], __builtin_amdgcn_s_memtime() - tx0);
+#endif
             }
             __syncthreads();
             if (row < r1) {
