@@ -158,6 +158,25 @@ def bench_qmm(steps, warmup, dev):
             "config": {"workload": "qmm", "M": M, "K": K, "N": N}}
 
 
+def bench_vendor(steps, warmup, dev):
+    """Context for the GEMM figures: the vendor int8 GEMM (torch._int_mm -> hipBLASLt, int32 out, no
+    epilogue) on the QuantMatmul shape, with the weight as the operator receives it (N contiguous)
+    and pre-transposed (K contiguous, a layout the drop-in boundary does not hand over)."""
+    d = cfgs.make_qmm(dev)
+    x1, x2 = d["x1"], d["x2"]
+    M, K = x1.shape
+    N = x2.shape[1]
+    ops = 2.0 * M * K * N
+    res = {"op": "torch._int_mm (hipBLASLt)", "M": M, "K": K, "N": N}
+    for name, w in (("n_contiguous", x2), ("k_contiguous", x2.t().contiguous().t())):
+        try:
+            ms = time_op(lambda: torch._int_mm(x1, w), steps, warmup)
+            res[name] = {"tops": round(ops / (ms * 1e-3) / 1e12, 1), "ms": round(ms, 4)}
+        except Exception as exc:  # reported, not fatal: the vendor path is context only
+            res[name] = {"error": str(exc).splitlines()[0][:200]}
+    return res
+
+
 def _hbm_entry(fn, nbytes, steps, warmup, config):
     """value: algorithmic bytes / wall time of the whole op call (host wrapper included);
     roofline: the same bytes / device time of the op's kernels (HIP events on its stream)."""
@@ -262,8 +281,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", default="prefill,decode,ardq,qmm,routing",
-                    help="comma list of prefill, decode, ardq, qmm, routing, copy")
+    ap.add_argument("--only", default="prefill,decode,ardq,qmm,routing,vendor",
+                    help="comma list of prefill, decode, ardq, qmm, routing, vendor, copy")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -306,6 +325,8 @@ def main():
                       "roofline": q["roofline"], "config": q["config"]}
     if "routing" in only:
         out["routing"] = bench_routing(args.steps, args.warmup, dev)
+    if "vendor" in only:
+        out["vendor_int8_gemm"] = bench_vendor(args.steps, args.warmup, dev)
     if "copy" in only:
         c = bench_copy(args.steps, args.warmup, dev)
         out["copy"] = {"value": round(c["gbs"], 1), "unit": "GB/s", "ms_per_step": round(c["ms"], 4),

@@ -357,7 +357,7 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
             for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) sum += acc[fm][fn][r];
-        if (sum == 0x7654321) ((int*)e.out)[tid] = sum;
+        asm volatile("" ::"v"(sum));  // keeps the accumulators live without a store
         return;
     }
 #endif
