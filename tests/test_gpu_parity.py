@@ -164,6 +164,25 @@ def test_gmsq(cb, orc, counts, K, N):
     assert_int8_close(np_i8(y), yr, label="gmsq y")
 
 
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_gmsq_fused_random_routing(cb, orc, seed):
+    """The persistent fused-requant GEMM with its 256-workgroup slot mapping (N = 4096: 16 column
+    tiles): 256 experts with ragged random counts (a third of them empty, some above 256 rows), so
+    row-tile counts are not a multiple of 4 and the last round has workgroups past the end.
+    Every row is compared with the oracle."""
+    rng = np.random.default_rng(100 + seed)
+    counts = rng.integers(0, 120, size=256)
+    counts[rng.random(256) < 0.33] = 0
+    counts[rng.integers(0, 256, size=3)] = rng.integers(257, 700, size=3)
+    counts = [int(c) for c in counts]
+    x, w, ws, xs, gl = _gmsq_inputs(counts, 256, 4096, 40 + seed)
+    y, ys = cb.grouped_matmul_swiglu_quant(x, w, ws, xs, gl)
+    torch.cuda.synchronize()
+    yr, ysr = orc.gmsq(np_i8(x), np_i8(w), ws.cpu().numpy(), xs.cpu().numpy(), np.array(gl))
+    np.testing.assert_allclose(ys.cpu().numpy(), ysr, rtol=1e-5)
+    assert_int8_close(np_i8(y), yr, label=f"gmsq random routing seed {seed}")
+
+
 def test_gmsq_zero_rows(cb):
     x, w, ws, xs, gl = _gmsq_inputs([5, 3], 256, 512, 1)
     x[2:4] = 0
