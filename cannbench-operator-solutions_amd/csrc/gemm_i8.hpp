@@ -82,7 +82,7 @@ struct GemmArgs {
     int64_t x_bstride, w_bstride;  // batch strides (dense QuantMatmul)
     int64_t w_gstride;             // group stride of the weight (K * N)
     int32_t ntiles;                // tiles along N
-    int32_t pad;
+    int32_t xcd_split;             // skinny kernel: XCDs sharing a group's column tiles (0: none)
     EpiArgs epi;
     GroupTable gt;
 };
@@ -198,9 +198,6 @@ __device__ __forceinline__ void set_comp(uint4& v, int i, u32 x)
 }
 
 // ============================================================================================
-#ifndef CB_SKINNY_XCD_MAP
-#define CB_SKINNY_XCD_MAP 1
-#endif
 // skinny_kernel: decode-shaped groups.
 //   grid = (ntiles, E), block = 256 (4 waves).  SwiGLU tiles cover 128 gate + 128 up columns,
 //   dequant tiles cover 256 columns.  Lane l of every wave owns k-group q = l / 16 and column
@@ -222,11 +219,13 @@ __global__ __launch_bounds__(256, PREFETCH ? 2 : CB_SKINNY_OCC) void skinny_kern
     // pieces.  Measured on a weight-streaming probe: 6.3 vs 5.5 TB/s.  Needs an even tile count
     // and a group count divisible by 4 (the host passes the grid as is otherwise).
     int g = blockIdx.y, ct = blockIdx.x;
-    if (CB_SKINNY_XCD_MAP && (gridDim.x & 1) == 0 && (gridDim.y & 3) == 0) {
+    const int P = a.xcd_split;  // XCDs sharing one group's column tiles (0: identity order)
+    if (P > 0) {
+        const int G = 8 / P;
         const int lin = blockIdx.y * gridDim.x + blockIdx.x;
-        const int x = lin & 7, j = lin >> 3, h = gridDim.x >> 1;
-        g = (j / h) * 4 + (x >> 1);
-        ct = (x & 1) * h + j % h;
+        const int x = lin & 7, j = lin >> 3, h = gridDim.x / P;
+        g = (j / h) * G + x / P;
+        ct = (x % P) * h + j % h;
     }
     const int r0 = g ? a.gt.row_end[g - 1] : 0;
     const int r1 = a.gt.row_end[g];

@@ -138,6 +138,18 @@ static void launch_gemm(GemmArgs& a, const int64_t* gl, int64_t E, int64_t batch
     if (a.gt.max_rows <= kSkinnyMaxRows) {
         a.ntiles = (int)((EPI == EPI_SWIGLU) ? (Ncols + 127) / 128 : (Ncols + 255) / 256);
         const dim3 grid((unsigned)a.ntiles, (unsigned)E, (unsigned)batch);
+        // XCD split: the most XCDs per group (4, 2, 1) that divide the column tiles and still give
+        // each XCD runs of at least 1 KB per weight row (measured best: decode 2, down-projection 4)
+        a.xcd_split = 0;
+        if (batch == 1) {
+            const int64_t tile_row_bytes = EPI == EPI_SWIGLU ? 128 : 256;
+            for (int P = 4; P >= 1; P >>= 1) {
+                if (a.ntiles % P == 0 && E % (8 / P) == 0 && (a.ntiles / P) * tile_row_bytes >= 1024) {
+                    a.xcd_split = P;
+                    break;
+                }
+            }
+        }
         hipLaunchKernelGGL((skinny_kernel<EPI, kSkinnyPrefetch>), grid, dim3(256), 0, st, a);
         return;
     }
