@@ -335,6 +335,7 @@ def main():
         out["roofline"]["traffic"] = traffic_from_profiles("prefill_gemm")
     if "decode" in out:
         out["decode"]["roofline"]["traffic"] = traffic_from_profiles("decode_gemm")
+        out["down_proj"]["roofline"]["traffic"] = traffic_from_profiles("down_proj_gemm")
     for name in ("finalize", "rerouting", "dqsq"):
         if name in out.get("routing", {}):
             out["routing"][name]["roofline"]["traffic"] = traffic_from_profiles("routing_" + name)
