@@ -62,6 +62,15 @@ __device__ __forceinline__ int rint16(float v)
     return (int)h;
 }
 
+// rint16 for v already clamped to [-128, 127] (so not NaN): fp16 rounding, fp16 round-half-even,
+// exact conversion - three instructions.  The result equals rint16(v): the fp16 value is exact in
+// fp32, and both round it half-to-even to the same integer in [-128, 127].
+__device__ __forceinline__ int rint16_inrange(float v)
+{
+    const _Float16 h = __builtin_elementwise_roundeven((_Float16)v);
+    return (int)(short)h;
+}
+
 __device__ __forceinline__ u32 pack4_i8(int a, int b, int c, int d)
 {
     return (u32)(a & 0xff) | ((u32)(b & 0xff) << 8) | ((u32)(c & 0xff) << 16) | ((u32)(d & 0xff) << 24);

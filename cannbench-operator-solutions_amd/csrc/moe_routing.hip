@@ -540,12 +540,12 @@ __global__ __launch_bounds__(512) void dqsq_kernel(const void* __restrict__ x, i
 #pragma unroll
         for (int u = 0; u < kDqsqMaxPerThread; ++u) {
             const int64_t j = (int64_t)u * blockDim.x + threadIdx.x;
-            if (j < H) y[r * H + j] = (int8_t)rint16(fminf(fmaxf(out[u] * inv, -128.0f), 127.0f));
+            if (j < H) y[r * H + j] = (int8_t)rint16_inrange(fminf(fmaxf(out[u] * inv, -128.0f), 127.0f));
         }
     } else {
         for (int64_t j = threadIdx.x; j < H; j += blockDim.x) {
             const float o = dqsq_elem<XDT>(x, base, H, j, ws, asr, qs, act_left);
-            y[r * H + j] = (int8_t)rint16(fminf(fmaxf(o * inv, -128.0f), 127.0f));
+            y[r * H + j] = (int8_t)rint16_inrange(fminf(fmaxf(o * inv, -128.0f), 127.0f));
         }
     }
 }
@@ -658,7 +658,7 @@ __global__ __launch_bounds__(512) void dqsq_vec_kernel(const void* __restrict__ 
                 int8_t b[4];
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
-                    b[t] = (int8_t)rint16(fminf(fmaxf(out[u][q4 * 4 + t] * inv, -128.0f), 127.0f));
+                    b[t] = (int8_t)rint16_inrange(fminf(fmaxf(out[u][q4 * 4 + t] * inv, -128.0f), 127.0f));
                 w[q4] = pack4_i8(b[0], b[1], b[2], b[3]);
             }
             if constexpr (V == 4) {
