@@ -177,6 +177,34 @@ def bench_vendor(steps, warmup, dev):
     return res
 
 
+def bench_mfma_probe(dev, iters=20000):
+    """Context for the int8 roofline: the matrix-core rate this device sustains with no memory
+    traffic (cb_probe_mfma_i8: independent 32x32x32 int8 MFMA chains on every CU), timed with HIP
+    events around the kernel.  The published 5.0 POPS assumes the peak clock; this is what the part
+    delivers at the clock it holds under MFMA load."""
+    import ctypes
+    lib = L.load()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.zeros(8 * cus, dtype=torch.int32, device=dev)
+    ops = ctypes.c_int64(0)
+    st = torch.cuda.current_stream().cuda_stream
+    best = None
+    for _ in range(4):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(); b.record()
+        torch.cuda.synchronize()
+        lib.cb_set_kernel_timing(a.cuda_event, b.cuda_event)
+        rc = lib.cb_probe_mfma_i8(iters, sink.data_ptr(), sink.numel(), ctypes.byref(ops), st)
+        if rc != 0:
+            return {"error": L.status_string(rc)}
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b)
+        best = ms if best is None else min(best, ms)
+    tops = ops.value / (best * 1e-3) / 1e12
+    return {"tops": round(tops, 1), "frac_of_published_peak": round(tops / PEAK_INT8_TOPS, 4), "ms": round(best, 4),
+            "kernel": "cb_probe_mfma_i8", "iters": iters}
+
+
 def _hbm_entry(fn, nbytes, steps, warmup, config):
     """value: algorithmic bytes / wall time of the whole op call (host wrapper included);
     roofline: the same bytes / device time of the op's kernels (HIP events on its stream)."""
@@ -327,6 +355,7 @@ def main():
         out["routing"] = bench_routing(args.steps, args.warmup, dev)
     if "vendor" in only:
         out["vendor_int8_gemm"] = bench_vendor(args.steps, args.warmup, dev)
+        out["mfma_probe"] = bench_mfma_probe(dev)
     if "copy" in only:
         c = bench_copy(args.steps, args.warmup, dev)
         out["copy"] = {"value": round(c["gbs"], 1), "unit": "GB/s", "ms_per_step": round(c["ms"], 4),

@@ -49,6 +49,7 @@ SIGNATURES = {
     "cb_status_string": (ctypes.c_char_p, [_I]),
     "cb_version": (ctypes.c_char_p, []),
     "cb_set_kernel_timing": (None, [_P, _P]),
+    "cb_probe_mfma_i8": (_I, [_I64, _P, _I64, _P, _P]),
     "cb_add_rms_norm_dynamic_quant": (_I, [_P, _P, _P, _I, _I64, _I64, _F, _P, _P, _P, _P]),
     "cb_dynamic_quant": (_I, [_P, _I, _I64, _I64, _P, _P, _P]),
     "cb_grouped_matmul_swiglu_quant_workspace_size": (_I64, [_I64, _I64, _I64, _I64]),

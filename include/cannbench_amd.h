@@ -82,6 +82,16 @@ const char* cb_version(void);
 void cb_set_kernel_timing(void* start_event, void* stop_event);
 
 /*
+ * Measurement (no reference counterpart): the int8 matrix-core rate the device sustains.  Launches
+ * 2 workgroups of 4 waves per CU, each wave issuing `iters` rounds of 8 independent
+ * v_mfma_i32_32x32x32_i8 on register operands (no memory traffic), and stores the total operation
+ * count (2 * 32 * 32 * 32 per MFMA) in *ops.  `sink` (at least 8 int32 per CU, device memory)
+ * receives checksums that keep the work live.  Time it with cb_set_kernel_timing.
+ * Returns CB_ERR_SHAPE for iters <= 0 or a short sink.
+ */
+int cb_probe_mfma_i8(int64_t iters, int32_t* sink, int64_t sink_len, int64_t* ops, void* stream);
+
+/*
  * AddRmsNormDynamicQuant.
  * Replaces add_rms_norm_dynamic_quant(Tensor x1, Tensor x2, Tensor gamma, float epsilon)
  *   -> (Tensor y, Tensor xOut, Tensor scaleOut)

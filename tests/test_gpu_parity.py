@@ -339,3 +339,25 @@ def test_torch_ops_registration(cb):
     y1, ys1 = torch.ops.cann_bench.grouped_matmul_swiglu_quant(x, w, ws, xs, gl)
     y2, ys2 = cb.grouped_matmul_swiglu_quant(x, w, ws, xs, gl)
     assert torch.equal(y1, y2) and torch.equal(ys1, ys2)
+
+
+def test_mfma_probe_runs_and_is_deterministic(cb):
+    """The measurement kernel: status ok, the operation count it reports, identical checksums on
+    two runs, and the sink-length check."""
+    import ctypes
+    import importlib
+    L = importlib.import_module("cannbench-operator-solutions_amd._lib")
+    lib = L.load()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.zeros(8 * cus, dtype=torch.int32, device=DEV)
+    ops = ctypes.c_int64(0)
+    st = torch.cuda.current_stream().cuda_stream
+    assert lib.cb_probe_mfma_i8(10, sink.data_ptr(), sink.numel(), ctypes.byref(ops), st) == L.CB_OK
+    torch.cuda.synchronize()
+    assert ops.value == 2 * cus * 4 * 10 * 8 * 2 * 32 * 32 * 32
+    first = sink.clone()
+    assert lib.cb_probe_mfma_i8(10, sink.data_ptr(), sink.numel(), ctypes.byref(ops), st) == L.CB_OK
+    torch.cuda.synchronize()
+    assert torch.equal(first, sink)
+    assert lib.cb_probe_mfma_i8(10, sink.data_ptr(), 8, ctypes.byref(ops), st) == L.CB_ERR_SHAPE
+    assert lib.cb_probe_mfma_i8(0, sink.data_ptr(), sink.numel(), ctypes.byref(ops), st) == L.CB_ERR_SHAPE
