@@ -5,6 +5,9 @@
 // plus the status strings.  Each entry point validates in the reference plugin's order, then
 // enqueues its kernels on the caller's stream without any allocation or host synchronisation.
 #include <cstring>
+#include <mutex>
+#include <set>
+#include <utility>
 
 #include "gemm_lds.hpp"
 
@@ -88,6 +91,19 @@ static int device_cus()
     return cus[dev];
 }
 
+// Raise a kernel's dynamic LDS limit once per (kernel, device): the attribute belongs to the
+// kernel as loaded on the current device, so a process driving several GPUs sets it on each.
+static void allow_dynamic_lds(const void* kern, int bytes)
+{
+    static std::mutex mu;
+    static std::set<std::pair<const void*, int>> done;
+    int dev = -1;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lock(mu);
+    if (done.insert({kern, dev}).second)
+        (void)hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+}
+
 static constexpr int kSkinnyMaxRows = 32;  // groups up to this many rows take the skinny core
 static constexpr int kTiledBM = 128;
 #ifndef CB_SKINNY_PREFETCH
@@ -159,11 +175,7 @@ static void launch_gemm(GemmArgs& a, const int64_t* gl, int64_t E, int64_t batch
         build_group_table(a.gt, gl, E, Cfg::BM);
         const int64_t blocks = (int64_t)a.gt.total_mtiles * a.ntiles;
         auto kern = lds_gemm_kernel<EPI, kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
-        static bool attr_set = false;  // per template instance; idempotent, so a benign race
-        if (!attr_set) {
-            (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS_BYTES);
-            attr_set = true;
-        }
+        allow_dynamic_lds((const void*)kern, Cfg::LDS_BYTES);
         hipLaunchKernelGGL(kern, dim3((unsigned)blocks, (unsigned)batch), dim3(Cfg::NT), Cfg::LDS_BYTES, st, a);
         return;
     }
@@ -272,11 +284,7 @@ extern "C" int cb_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* wei
             fill_u32(amax, (ws.status_off - ws.amax_off) / 4 + 1, 0u, st);
             using Cfg = LdsCfg<kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
             auto kern = lds_gemm_swiglu_q_kernel<kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
-            static bool attr_set = false;  // idempotent, so a benign race
-            if (!attr_set) {
-                (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS_BYTES);
-                attr_set = true;
-            }
+            allow_dynamic_lds((const void*)kern, Cfg::LDS_BYTES);
             TimedLaunch timed(st);
             hipLaunchKernelGGL(kern, dim3((unsigned)(slots * ntl)), dim3(Cfg::NT), Cfg::LDS_BYTES, st, a);
             return check_launch();
