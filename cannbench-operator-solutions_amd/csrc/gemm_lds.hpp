@@ -27,8 +27,10 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 #define CB_LDS __attribute__((address_space(3)))
 
 // Polls of a row tile's arrival counter before the fused requant gives up (each poll sleeps about
-// 512 cycles plus an atomic round trip: a few hundred ms in total, against microseconds normally).
-constexpr int kExchangeSpinLimit = 1 << 16;
+// 512 cycles plus an atomic round trip: about 2 s in total, against microseconds normally; long
+// enough for kernels on other streams that hold CUs to drain before the grid is all resident).
+// A timeout sets the workspace status word (cb_grouped_matmul_swiglu_quant_status).
+constexpr int kExchangeSpinLimit = 1 << 20;
 
 // The LDS DMA and the stage barrier are written as inline asm on purpose: when the compiler sees
 // buffer_load ... lds it must assume every later LDS read may alias the DMA target and waits for

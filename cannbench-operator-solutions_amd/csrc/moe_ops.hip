@@ -290,10 +290,27 @@ extern "C" int cb_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* wei
             return check_launch();
         }
     }
-    fill_u32(amax, M, 0u, st);
+    // row maxima and the status word start at zero on this path too
+    fill_u32(amax, (ws.status_off - ws.amax_off) / 4 + 2, 0u, st);
     launch_gemm<EPI_SWIGLU>(a, group_list, E, 1, fast, st);
     hipLaunchKernelGGL(gmsq_requant_kernel, dim3((unsigned)M), dim3(256), 0, st, act, amax, H, y, y_scale);
     return check_launch();
+}
+
+extern "C" int cb_grouped_matmul_swiglu_quant_status(const void* workspace, int64_t M, int64_t N, int64_t E,
+                                                     uint32_t* status, void* stream)
+{
+    if (!workspace || !status) return CB_ERR_NULL_POINTER;
+    if (M <= 0 || N <= 0 || E <= 0) {
+        *status = 0;  // no launch happened
+        return CB_OK;
+    }
+    const GmsqWorkspace ws = gmsq_workspace(M, N, E);
+    hipStream_t st = (hipStream_t)stream;
+    if (hipMemcpyAsync(status, (const uint8_t*)workspace + ws.status_off, 4, hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+        return CB_ERR_LAUNCH;
+    return CB_OK;
 }
 
 extern "C" int cb_grouped_matmul_quant(const int8_t* x, const int8_t* weight, const float* weight_scale,

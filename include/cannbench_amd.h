@@ -140,6 +140,16 @@ int cb_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* weight, const 
                                    int64_t workspace_bytes, void* stream);
 
 /*
+ * Validation (no reference counterpart): the status word a GroupedMatmulSwigluQuant call left in
+ * `workspace` (the same M, N, E).  0: every per-row maximum was complete when the row was
+ * quantised.  1: a row-max exchange of the persistent kernel timed out (its workgroups could not
+ * all be resident together within about 2 s) and some rows were quantised with a partial maximum.
+ * Synchronises `stream`, so it is meant for tests and debug runs, not the hot loop.
+ */
+int cb_grouped_matmul_swiglu_quant_status(const void* workspace, int64_t M, int64_t N, int64_t E,
+                                          uint32_t* status, void* stream);
+
+/*
  * QuantMatmul (dense W8A8 with dequant epilogue).
  * Replaces quant_matmul(Tensor x1, Tensor x2, Tensor scale, *, Tensor? offset=None,
  *   Tensor? pertoken_scale=None, Tensor? bias=None, str? output_dtype=None) -> Tensor

@@ -5,6 +5,8 @@ import sys
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+# GroupedMatmulSwigluQuant calls in the tests read back the persistent kernel's status word
+os.environ.setdefault("CANNBENCH_AMD_CHECK", "1")
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 

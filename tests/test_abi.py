@@ -153,3 +153,15 @@ def test_routing_validation(lib):
     assert so.cb_moe_gating_top_k_softmax(FAKE, 3, 4, 8, None, 9, FAKE, FAKE, FAKE, None) == L.CB_ERR_SHAPE
     assert so.cb_moe_gating_top_k_softmax(FAKE, 3, 4, 4096, None, 2, FAKE, FAKE, FAKE, None) == L.CB_ERR_SHAPE
     assert so.cb_moe_gating_top_k_softmax(FAKE, 3, 0, 8, None, 2, FAKE, FAKE, FAKE, None) == L.CB_ERR_EMPTY
+
+
+def test_gmsq_status_query_host_paths(lib):
+    """The status query rejects NULL arguments and reports 0 for empty shapes, both before any
+    device access."""
+    L, so = lib
+    st = ctypes.c_uint32(7)
+    assert so.cb_grouped_matmul_swiglu_quant_status(None, 16, 64, 2, ctypes.byref(st), None) == L.CB_ERR_NULL_POINTER
+    buf = (ctypes.c_uint8 * 16)()
+    assert so.cb_grouped_matmul_swiglu_quant_status(ctypes.addressof(buf), 16, 64, 2, None, None) == L.CB_ERR_NULL_POINTER
+    assert so.cb_grouped_matmul_swiglu_quant_status(ctypes.addressof(buf), 0, 64, 2, ctypes.byref(st), None) == L.CB_OK
+    assert st.value == 0
