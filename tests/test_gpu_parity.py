@@ -139,6 +139,8 @@ GMSQ_CASES = [
     ([1], 512, 256),                           # single row, E = 1
     ([200, 0, 37, 129, 1], 1024, 512),         # tiled, ragged
     ([640], 256, 1024),                        # all rows in one expert, E = 1
+    ([100, 300, 37], 400, 896),                # fused persistent path: K tail (400 = 3 x 128 + 16), H = 448 (last column tile half full)
+    ([260, 0, 33], 7184, 4128),                # fused path: K = 7168 + 16, H = 2064 (17 column tiles, the last 16 columns wide)
     ([6, 11], 80, 48),                         # K % 16 == 0, H = 24 not a multiple of 16 -> generic
     ([4, 4], 40, 64),                          # K % 16 != 0 -> generic
 ]
@@ -281,6 +283,7 @@ def test_quant_matmul_flags(cb, orc, variant):
 # int8 grouped down-projection
 # ---------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("counts,K,N", [([3, 0, 5, 1, 16, 0, 2, 8], 2048, 7168), ([300, 0, 45], 512, 768),
+                                        ([270, 40], 400, 784),
                                         ([5, 6], 40, 64)])
 def test_grouped_matmul_quant(cb, orc, counts, K, N):
     g = cpu_gen(K + N)
