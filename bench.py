@@ -93,6 +93,40 @@ def bench_prefill(steps, warmup, dev, keep):
     return res
 
 
+def bench_prefill_gather(steps, warmup, dev, keep):
+    """GroupedMatmulSwigluQuant with gathered rows on the MoE prefill flow: 16384 tokens x 7168 (the
+    first rows of the prefill activations), 131072 routed rows over the prefill config's Zipf expert
+    counts, each routed row naming a seeded-random source token (about 8 routed rows per token).
+    Against the unfused sequence: an explicit gather (torch index_select) of the 131072 rows and their
+    scales, then the plain operator."""
+    d = keep["prefill"]
+    T = 16384
+    x_tok, xs_tok = d["x"][:T], d["x_scale"][:T]
+    M, K = d["x"].shape
+    N = d["weight"].shape[2]
+    g = torch.Generator(device=dev)
+    g.manual_seed(21)
+    idx = torch.randint(0, T, (M,), generator=g, dtype=torch.int32, device=dev)
+    # a stable sort of the (token, slot) pairs by expert leaves each expert's token ids ascending
+    bounds = [0] + list(d["group_list"])
+    idx = torch.cat([idx[s:e].sort().values for s, e in zip(bounds[:-1], bounds[1:])])
+    ops = 2.0 * M * K * N
+    fused = lambda: cb.grouped_matmul_swiglu_quant_gather(x_tok, idx, d["weight"], d["weight_scale"], xs_tok,
+                                                          d["group_list"])
+    timer = KernelTimer(steps)
+    ms = time_op(fused, steps, warmup, timer)
+    kms = timer.mean_ms()
+    il = idx.long()
+    unfused = lambda: cb.grouped_matmul_swiglu_quant(x_tok.index_select(0, il), d["weight"], d["weight_scale"],
+                                                     xs_tok.index_select(0, il), d["group_list"])
+    ms_u = time_op(unfused, steps, warmup)
+    return {"value": round(ops / (ms * 1e-3) / 1e12, 2), "unit": "TOPS", "ms_per_step": round(ms, 4),
+            "gemm_kernel_ms": round(kms, 4), "roofline": roofline("mfma", ops / (kms * 1e-3) / 1e12, "TFLOP/s"),
+            "unfused_ms_per_step": round(ms_u, 4), "saving_ms": round(ms_u - ms, 4),
+            "config": {"workload": "gmsq_prefill_gather", "tokens": T, "rows": M, "experts": len(d["group_list"]),
+                       "K": K, "N": N, "row_index": "uniform random source token per routed row (torch seed 21), ascending within each expert"}}
+
+
 def decode_bytes(counts, K, N):
     M = int(np.sum(counts))
     act = int(np.sum(np.asarray(counts) > 0))
@@ -309,8 +343,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", default="prefill,decode,ardq,qmm,routing,vendor",
-                    help="comma list of prefill, decode, ardq, qmm, routing, vendor, copy")
+    ap.add_argument("--only", default="prefill,gather,decode,ardq,qmm,routing,vendor",
+                    help="comma list of prefill, gather (needs prefill), decode, ardq, qmm, routing, vendor, copy")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -334,6 +368,8 @@ def main():
                    roofline=p["roofline"])
         out["prefill_gemm_kernel_ms"] = round(p["gemm_kernel_ms"], 4)
         out["frac_of_int8_peak"] = round(p["tops"] / PEAK_INT8_TOPS, 4)
+        if "gather" in only:
+            out["prefill_gather"] = bench_prefill_gather(args.steps, args.warmup, dev, keep)
     if "decode" in only:
         keep.pop("prefill_tensors", None)
         dres, down = bench_decode(args.steps, args.warmup, dev, keep)

@@ -9,7 +9,7 @@ compute runs in hand-written HIP kernels behind the C ABI of include/cannbench_a
 `register_torch_ops()` additionally exposes them as torch.ops.cann_bench.*.
 """
 from .ops import (add_rms_norm_dynamic_quant, dynamic_quant, grouped_matmul_int32, grouped_matmul_quant,
-                  grouped_matmul_swiglu_quant, quant_matmul, moe_re_routing, moe_finalize_routing,
+                  grouped_matmul_swiglu_quant, grouped_matmul_swiglu_quant_gather, quant_matmul, moe_re_routing, moe_finalize_routing,
                   dequant_swiglu_quant, moe_gating_top_k_softmax)
 from . import _lib
 
@@ -23,6 +23,7 @@ def library_path():
     return _lib.LIB_PATH
 
 
-__all__ = ["add_rms_norm_dynamic_quant", "dynamic_quant", "grouped_matmul_swiglu_quant", "quant_matmul",
+__all__ = ["add_rms_norm_dynamic_quant", "dynamic_quant", "grouped_matmul_swiglu_quant",
+           "grouped_matmul_swiglu_quant_gather", "quant_matmul",
            "grouped_matmul_quant", "grouped_matmul_int32", "moe_re_routing", "moe_finalize_routing", "dequant_swiglu_quant",
            "moe_gating_top_k_softmax", "register_torch_ops", "library_path"]

@@ -55,6 +55,7 @@ SIGNATURES = {
     "cb_grouped_matmul_swiglu_quant_workspace_size": (_I64, [_I64, _I64, _I64, _I64]),
     "cb_grouped_matmul_swiglu_quant": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P]),
     "cb_grouped_matmul_swiglu_quant_status": (_I, [_P, _I64, _I64, _I64, _P, _P]),
+    "cb_grouped_matmul_swiglu_quant_gather": (_I, [_P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P]),
     "cb_quant_matmul": (_I, [_P, _P, _P, _I, _I64, _P, _I64, _P, _I64, _P, _I, _I64, _I, _I64, _I64, _I64, _I64, _I, _P, _P]),
     "cb_grouped_matmul_quant": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P]),
     "cb_grouped_matmul_int32": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P]),

@@ -83,9 +83,28 @@ struct GemmArgs {
     int64_t w_gstride;             // group stride of the weight (K * N)
     int32_t ntiles;                // tiles along N
     int32_t xcd_split;             // skinny kernel: XCDs sharing a group's column tiles (0: none)
+    // Gathered activation rows (GroupedMatmulSwigluQuant with a row index): routed row r reads
+    // x row row_index[r] and x_scale[row_index[r]], x holding x_rows rows.  NULL: row r is x row r.
+    const int32_t* row_index;
+    int64_t x_rows;
     EpiArgs epi;
     GroupTable gt;
 };
+
+// Source row of routed row r: r itself, or row_index[r]; -1 when the index lies outside
+// [0, x_rows) (such a row reads as zeros with scale 0).
+__device__ __forceinline__ int src_row(const GemmArgs& a, int r)
+{
+    if (!a.row_index) return r;
+    const int s = a.row_index[r];
+    return (unsigned)s < (unsigned)a.x_rows ? s : -1;
+}
+
+__device__ __forceinline__ float src_x_scale(const GemmArgs& a, int r)
+{
+    const int s = src_row(a, r);
+    return s >= 0 ? a.epi.x_scale[s] : 0.0f;
+}
 
 __device__ __forceinline__ float load_scalar_any(const void* p, int kind, int64_t i)
 {
@@ -261,11 +280,13 @@ __global__ __launch_bounds__(256, PREFETCH ? 2 : CB_SKINNY_OCC) void skinny_kern
         for (int j = 0; j < 16; ++j) acc[j] = v4i{0, 0, 0, 0};
 
         const int arow = mb + c;
-        const bool arow_ok = arow < r1;
-        // activation row of this lane through a buffer resource: rows past the group and k past K
-        // read as zeros without a branch, so the activation load joins its chunk's weight loads
+        const int asrc = arow < r1 ? src_row(a, arow) : -1;
+        const bool arow_ok = asrc >= 0;
+        // activation row of this lane through a buffer resource: rows past the group (or gathered
+        // from outside x) and k past K read as zeros without a branch, so the activation load joins
+        // its chunk's weight loads
         const __amdgpu_buffer_rsrc_t xres =
-            make_rsrc(a.x + b * a.x_bstride + (int64_t)(arow_ok ? arow : r0) * K, arow_ok ? (uint32_t)K : 0u);
+            make_rsrc(a.x + b * a.x_bstride + (int64_t)(arow_ok ? asrc : 0) * K, arow_ok ? (uint32_t)K : 0u);
 
         // one chunk = the activation operand (first, so waiting for it never waits for weights
         // issued later) and 16 weight rows
@@ -355,7 +376,7 @@ __global__ __launch_bounds__(256, PREFETCH ? 2 : CB_SKINNY_OCC) void skinny_kern
             for (int j = 0; j < 16; ++j) u[j] = __shfl_xor(s[j], 8, 64);
             float m = 0.0f;
             if (c < 8 && rowok && colok) {
-                const float xs = e.x_scale[row];
+                const float xs = src_x_scale(a, row);
                 const float* wsg = e.w_scale + (int64_t)g * N + opaque(ocol);
                 const float* wsu = wsg + H;
                 float act[16];
@@ -476,7 +497,8 @@ __global__ __launch_bounds__(256, 1) void tiled_kernel(const GemmArgs a)
         const int id = tid + 256 * i;
         int row = m0 + (id >> 2);
         row = row < r1 ? row : r1 - 1;
-        a_src[i] = xb + (int64_t)row * K + (id & 3) * 16;
+        const int srow = src_row(a, row);  // an out-of-range gathered row reads row 0, scaled by 0
+        a_src[i] = xb + (int64_t)(srow >= 0 ? srow : 0) * K + (id & 3) * 16;
     }
     // B: thread -> 8 k rows (8 rg .. 8 rg + 7) x 8 tile columns (8 cg .. 8 cg + 7)
     const int rg = tid & 7, cg = tid >> 3;
@@ -614,7 +636,7 @@ __global__ __launch_bounds__(256, 1) void tiled_kernel(const GemmArgs a)
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm * TM + fm * 32 + (r >> 2) * 8 + lr + (r & 3);
                 const bool rowok = row < r1;
-                const float xs = rowok ? e.x_scale[row] : 0.0f;
+                const float xs = rowok ? src_x_scale(a, row) : 0.0f;
                 float m = 0.0f;
 #pragma unroll
                 for (int fn = 0; fn < FN / 2; ++fn) {
@@ -701,15 +723,16 @@ __global__ __launch_bounds__(256) void generic_swiglu_kernel(const GemmArgs a)
     const int g = group_of_row(a.gt, row);
     float v = 0.0f;
     if (ok) {
-        const int8_t* xr = a.x + (int64_t)row * a.K;
+        const int srow = src_row(a, row);
+        const int8_t* xr = a.x + (int64_t)(srow >= 0 ? srow : 0) * a.K;
         const int8_t* wg = a.w + (int64_t)g * a.w_gstride;
         int cg = 0, cu = 0;
         for (int64_t k = 0; k < a.K; ++k) {
-            const int xv = xr[k];
+            const int xv = srow >= 0 ? xr[k] : 0;
             cg += xv * (int)wg[k * a.N + idx];
             cu += xv * (int)wg[k * a.N + H + idx];
         }
-        v = swiglu((float)cg, (float)cu, a.epi.x_scale[row], a.epi.w_scale[(int64_t)g * a.N + idx],
+        v = swiglu((float)cg, (float)cu, src_x_scale(a, row), a.epi.w_scale[(int64_t)g * a.N + idx],
                    a.epi.w_scale[(int64_t)g * a.N + H + idx]);
         a.epi.act[(int64_t)row * H + idx] = v;
     }

@@ -116,9 +116,12 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
     const int m0 = rs + (mt - a.gt.tile_start[g]) * BM;
     const int vrows = r1 - m0;  // valid rows of this tile (>= 1)
 
-    // buffer resources: A = rows [m0, r1) of x, B = this group's weight [K, N]
+    // buffer resources: A = rows [m0, r1) of x (with a row index: all of x, rows gathered through
+    // the per-lane DMA offsets), B = this group's weight [K, N]
+    const bool gather = a.row_index != nullptr;
     const __amdgpu_buffer_rsrc_t ares =
-        make_rsrc(a.x + b * a.x_bstride + (int64_t)m0 * K, (uint32_t)((int64_t)vrows * K));
+        gather ? make_rsrc(a.x, (uint32_t)(a.x_rows * K))
+               : make_rsrc(a.x + b * a.x_bstride + (int64_t)m0 * K, (uint32_t)((int64_t)vrows * K));
     const __amdgpu_buffer_rsrc_t bres =
         make_rsrc(a.w + b * a.w_bstride + (int64_t)g * a.w_gstride, (uint32_t)(K * N));
 
@@ -129,9 +132,10 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
         const int cid = (i * NW + wave) * 64 + lane;  // 16-byte chunk id in the A tile
         const int row = cid / ACH, pos = cid % ACH;
         const int q = pos ^ a_swz(row);
-        // rows past the tile's valid rows point past the resource: they read zeros and fetch
-        // nothing, so a partial tile moves only its valid rows
-        a_off[i] = row < vrows ? (uint32_t)row * (uint32_t)K + (uint32_t)(q * 16) : 0x80000000u;
+        // rows past the tile's valid rows (and gathered rows outside x) point past the resource:
+        // they read zeros and fetch nothing, so a partial tile moves only its valid rows
+        const int srow = row < vrows ? (gather ? src_row(a, m0 + row) : row) : -1;
+        a_off[i] = srow >= 0 ? (uint32_t)srow * (uint32_t)K + (uint32_t)(q * 16) : 0x80000000u;
     }
     uint32_t b_off[C::B_ISSUE];
 #pragma unroll
@@ -386,7 +390,7 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
             for (int r = 0; r < 16; ++r) {
                 const int lrow = (WM * fm + wm) * 32 + (r >> 2) * 8 + lr + (r & 3);
                 const int row = m0 + lrow < r1 ? m0 + lrow : r1 - 1;
-                const float xs = e.x_scale[row];
+                const float xs = src_x_scale(a, row);
 #pragma unroll
                 for (int fn = 0; fn < FN / 2; ++fn) {
                     const float v = swiglu((float)acc[fm][fn][r], (float)acc[fm][fn + FN / 2][r], xs, wsg[fn], wsu[fn]);

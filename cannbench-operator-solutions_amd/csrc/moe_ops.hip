@@ -227,17 +227,20 @@ extern "C" int64_t cb_grouped_matmul_swiglu_quant_workspace_size(int64_t M, int6
     return gmsq_workspace(M, N, E).total;
 }
 
-extern "C" int cb_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* weight, const float* weight_scale,
-                                              const float* x_scale, const int64_t* group_list,
-                                              int64_t group_len, int64_t M, int64_t K, int64_t N, int64_t E,
-                                              int8_t* y, float* y_scale, void* workspace,
-                                              int64_t workspace_bytes, void* stream)
+// GroupedMatmulSwigluQuant, optionally with the activation rows gathered through row_index (x then
+// holds x_rows rows, x_scale x_rows scales).
+static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, const int8_t* weight,
+                     const float* weight_scale, const float* x_scale, const int64_t* group_list,
+                     int64_t group_len, int64_t M, int64_t K, int64_t N, int64_t E, int8_t* y,
+                     float* y_scale, void* workspace, int64_t workspace_bytes, void* stream)
 {
-    if (M < 0 || K < 0 || N < 0 || E < 0) return CB_ERR_SHAPE;
+    if (M < 0 || K < 0 || N < 0 || E < 0 || x_rows < 0) return CB_ERR_SHAPE;
     if (N % 2 != 0) return CB_ERR_N_ODD;  // GmsqMeta checks this before anything else
     if (M == 0 || N == 0 || E == 0) return CB_OK;  // gmsq_plugin.cpp:93-95
     if (!x || !weight || !weight_scale || !x_scale || !y || !y_scale) return CB_ERR_NULL_POINTER;
     if (M > 0x7fffffffLL) return CB_ERR_SHAPE;
+    // gathered rows are addressed with 32-bit offsets into x
+    if (row_index && (x_rows == 0 || x_rows * K >= 0x7fffffffLL)) return CB_ERR_SHAPE;
     const int vs = validate_group_list(group_list, group_len, E, M);
     if (vs != CB_OK) return vs;
     const GmsqWorkspace ws = gmsq_workspace(M, N, E);
@@ -259,6 +262,8 @@ extern "C" int cb_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* wei
     a.K = K;
     a.N = N;
     a.w_gstride = K * N;
+    a.row_index = row_index;
+    a.x_rows = row_index ? x_rows : M;
     a.epi.w_scale = weight_scale;
     a.epi.x_scale = x_scale;
     a.epi.act = act;
@@ -295,6 +300,28 @@ extern "C" int cb_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* wei
     launch_gemm<EPI_SWIGLU>(a, group_list, E, 1, fast, st);
     hipLaunchKernelGGL(gmsq_requant_kernel, dim3((unsigned)M), dim3(256), 0, st, act, amax, H, y, y_scale);
     return check_launch();
+}
+
+extern "C" int cb_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* weight, const float* weight_scale,
+                                              const float* x_scale, const int64_t* group_list,
+                                              int64_t group_len, int64_t M, int64_t K, int64_t N, int64_t E,
+                                              int8_t* y, float* y_scale, void* workspace,
+                                              int64_t workspace_bytes, void* stream)
+{
+    return gmsq_impl(x, M, nullptr, weight, weight_scale, x_scale, group_list, group_len, M, K, N, E, y, y_scale,
+                     workspace, workspace_bytes, stream);
+}
+
+extern "C" int cb_grouped_matmul_swiglu_quant_gather(const int8_t* x, int64_t x_rows, const int32_t* row_index,
+                                                     const int8_t* weight, const float* weight_scale,
+                                                     const float* x_scale, const int64_t* group_list,
+                                                     int64_t group_len, int64_t M, int64_t K, int64_t N, int64_t E,
+                                                     int8_t* y, float* y_scale, void* workspace,
+                                                     int64_t workspace_bytes, void* stream)
+{
+    if (!row_index && M > 0 && N > 0 && E > 0) return CB_ERR_NULL_POINTER;
+    return gmsq_impl(x, x_rows, row_index, weight, weight_scale, x_scale, group_list, group_len, M, K, N, E, y,
+                     y_scale, workspace, workspace_bytes, stream);
 }
 
 extern "C" int cb_grouped_matmul_swiglu_quant_status(const void* workspace, int64_t M, int64_t N, int64_t E,

@@ -148,38 +148,47 @@ def _validate_group_list(prefix, group_list, E, M, max_e):
     return gl
 
 
-def grouped_matmul_swiglu_quant(x, weight, weight_scale, x_scale, group_list):
-    """(y int8 [M, N/2], y_scale fp32 [M]) = GroupedMatmulSwigluQuant(...).
-
-    group_list: python list / tensor of E int64 cumulative row counts (a host attribute).
-    """
-    name = "grouped_matmul_swiglu_quant"
+def _gmsq(name, x, row_index, weight, weight_scale, x_scale, group_list):
     _check(x.dtype == torch.int8, f"{name}: x must be int8")
     _check(weight.dtype == torch.int8, f"{name}: weight must be int8")
     _check(weight_scale.dtype == torch.float32, f"{name}: weight_scale must be float32")
     _check(x_scale.dtype == torch.float32, f"{name}: x_scale must be float32")
+    if row_index is not None:
+        _check(row_index.dtype == torch.int32 and row_index.dim() == 1, f"{name}: row_index must be 1D int32")
+        row_index = row_index.contiguous()
     x = x.contiguous()
     weight = weight.contiguous()
     weight_scale = weight_scale.contiguous()
     x_scale = x_scale.contiguous()
-    y, y_scale = grouped_matmul_swiglu_quant_meta(x, weight, weight_scale, x_scale, group_list)
-    M, K = x.shape
+    _check(x.dim() == 2, f"{name}: x must be 2D [M, K]")
+    _check(weight.dim() == 3, f"{name}: weight must be 3D [E, K, N]")
+    M = x.size(0) if row_index is None else row_index.numel()
+    _check(weight.size(2) % 2 == 0, f"{name}: N must be even")
+    y = torch.empty((M, weight.size(2) // 2), dtype=torch.int8, device=x.device)
+    y_scale = torch.empty((M,), dtype=torch.float32, device=x.device)
+    K = x.size(1)
     E, N = weight.size(0), weight.size(2)
     if M == 0 or N == 0 or E == 0:
         return y, y_scale
     _check(weight.size(1) == K, f"{name}: K mismatch between x and weight")
-    _check(x_scale.numel() == M, f"{name}: x_scale must have M elements")
+    _check(x_scale.numel() == x.size(0), f"{name}: x_scale must have M elements" if row_index is None
+           else f"{name}: x_scale must have one element per row of x")
     _check(weight_scale.dim() == 2 and weight_scale.size(0) == E and weight_scale.size(1) == N,
            f"{name}: weight_scale must be [E, N]")
     gl = _validate_group_list(name, group_list, E, M, L.CB_MAX_EXPERTS)
-    _on_device(name, x, weight, weight_scale, x_scale)
+    _on_device(name, x, weight, weight_scale, x_scale, row_index)
     lib = L.load()
     ws_bytes = lib.cb_grouped_matmul_swiglu_quant_workspace_size(M, K, N, E)
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=x.device)
     gla = L.int64_array(gl)
-    rc = lib.cb_grouped_matmul_swiglu_quant(
-        _ptr(x), _ptr(weight), _ptr(weight_scale), _ptr(x_scale), gla, len(gl), M, K, N, E,
-        _ptr(y), _ptr(y_scale), _ptr(ws), ws_bytes, _stream())
+    if row_index is None:
+        rc = lib.cb_grouped_matmul_swiglu_quant(
+            _ptr(x), _ptr(weight), _ptr(weight_scale), _ptr(x_scale), gla, len(gl), M, K, N, E,
+            _ptr(y), _ptr(y_scale), _ptr(ws), ws_bytes, _stream())
+    else:
+        rc = lib.cb_grouped_matmul_swiglu_quant_gather(
+            _ptr(x), x.size(0), _ptr(row_index), _ptr(weight), _ptr(weight_scale), _ptr(x_scale), gla, len(gl),
+            M, K, N, E, _ptr(y), _ptr(y_scale), _ptr(ws), ws_bytes, _stream())
     _raise_status(name, rc)
     if os.environ.get("CANNBENCH_AMD_CHECK") == "1":
         # validation runs: synchronise and fail if a row-max exchange timed out
@@ -187,6 +196,26 @@ def grouped_matmul_swiglu_quant(x, weight, weight_scale, x_scale, group_list):
         _raise_status(name, lib.cb_grouped_matmul_swiglu_quant_status(_ptr(ws), M, N, E, ctypes.byref(st), _stream()))
         _check(st.value == 0, f"{name}: the persistent kernel's row-max exchange timed out (status {st.value})")
     return y, y_scale
+
+
+def grouped_matmul_swiglu_quant(x, weight, weight_scale, x_scale, group_list):
+    """(y int8 [M, N/2], y_scale fp32 [M]) = GroupedMatmulSwigluQuant(...).
+
+    group_list: python list / tensor of E int64 cumulative row counts (a host attribute).
+    """
+    return _gmsq("grouped_matmul_swiglu_quant", x, None, weight, weight_scale, x_scale, group_list)
+
+
+def grouped_matmul_swiglu_quant_gather(x, row_index, weight, weight_scale, x_scale, group_list):
+    """GroupedMatmulSwigluQuant on gathered rows, without writing them: equal to
+    grouped_matmul_swiglu_quant(x[row_index], weight, weight_scale, x_scale[row_index], group_list).
+
+    x int8 [T, K] (e.g. one row per token), x_scale fp32 [T], row_index int32 [M] (the source row of
+    each routed row, e.g. MoeReRouting's permutation); outputs have M rows.  An index outside
+    [0, T) reads a zero row with scale 0.  No single reference op: it folds moe_re_routing's token
+    permutation (moe_re_routing_plugin.cpp:35-38) into the GEMM's activation loads.
+    """
+    return _gmsq("grouped_matmul_swiglu_quant_gather", x, row_index, weight, weight_scale, x_scale, group_list)
 
 
 # ------------------------------------------------------------------------------------------------

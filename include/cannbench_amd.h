@@ -140,6 +140,23 @@ int cb_grouped_matmul_swiglu_quant(const int8_t* x, const int8_t* weight, const 
                                    int64_t workspace_bytes, void* stream);
 
 /*
+ * GroupedMatmulSwigluQuant with the activation rows gathered (no single reference counterpart: it
+ * is the re-routing permutation of moe_re_routing, operators/moererouting/csrc/ops/moe_re_routing/
+ * op_plugin/moe_re_routing_plugin.cpp:35-38, folded into the GEMM's activation loads, so the
+ * permuted copy of the tokens is never written).  Routed row r (of M) computes with x row
+ * row_index[r] and x_scale[row_index[r]]; x holds x_rows rows [x_rows, K] and x_scale x_rows
+ * scales.  Output, group_list and workspace are those of cb_grouped_matmul_swiglu_quant for M rows,
+ * and the results equal that operator on the gathered rows.  An index outside [0, x_rows) reads a
+ * zero row with scale 0.  Requires x_rows * K < 2^31.
+ */
+int cb_grouped_matmul_swiglu_quant_gather(const int8_t* x, int64_t x_rows, const int32_t* row_index,
+                                          const int8_t* weight, const float* weight_scale,
+                                          const float* x_scale, const int64_t* group_list,
+                                          int64_t group_len, int64_t M, int64_t K, int64_t N, int64_t E,
+                                          int8_t* y, float* y_scale, void* workspace,
+                                          int64_t workspace_bytes, void* stream);
+
+/*
  * Validation (no reference counterpart): the status word a GroupedMatmulSwigluQuant call left in
  * `workspace` (the same M, N, E).  0: every per-row maximum was complete when the row was
  * quantised.  1: a row-max exchange of the persistent kernel timed out (its workgroups could not

@@ -364,3 +364,71 @@ def test_mfma_probe_runs_and_is_deterministic(cb):
     assert torch.equal(first, sink)
     assert lib.cb_probe_mfma_i8(10, sink.data_ptr(), 8, ctypes.byref(ops), st) == L.CB_ERR_SHAPE
     assert lib.cb_probe_mfma_i8(0, sink.data_ptr(), sink.numel(), ctypes.byref(ops), st) == L.CB_ERR_SHAPE
+
+
+# ---------------------------------------------------------------------------------------------
+# GroupedMatmulSwigluQuant with gathered activation rows
+# ---------------------------------------------------------------------------------------------
+def _random_256_counts(seed):
+    rng = np.random.default_rng(200 + seed)
+    counts = rng.integers(0, 120, size=256)
+    counts[rng.random(256) < 0.33] = 0
+    counts[rng.integers(0, 256, size=3)] = rng.integers(257, 700, size=3)
+    return [int(c) for c in counts]
+
+
+GATHER_CASES = [
+    # (counts, K, N, source rows T)  -- path exercised
+    ([3, 0, 5, 1, 16, 0, 2, 8], 7168, 4096, 20),   # skinny (decode-shaped), XCD-split order
+    ([200, 0, 37, 129, 1], 1024, 512, 150),       # persistent fused kernel
+    ([100, 300, 37], 400, 896, 90),               # persistent fused kernel, K tail, half column tile
+    (_random_256_counts(0), 256, 4096, 3000),     # persistent fused kernel, 256-workgroup slot mapping
+    ([6, 11], 80, 48, 9),                          # generic kernels
+]
+
+
+@pytest.mark.parametrize("counts,K,N,T", GATHER_CASES)
+def test_gmsq_gather_equals_explicit_gather(cb, counts, K, N, T):
+    """The gathered operator equals GroupedMatmulSwigluQuant on x[row_index], x_scale[row_index]:
+    the same kernels see the same values, so the results are identical."""
+    g = cpu_gen(T + K + N)
+    E, M = len(counts), sum(counts)
+    x = rand_i8((T, K), g)
+    w = rand_i8((E, K, N), g)
+    ws = (torch.rand(E, N, generator=g) * 0.009 + 0.001).to(DEV)
+    xs = (torch.rand(T, generator=g) * 0.015 + 0.005).to(DEV)
+    idx = torch.randint(0, T, (M,), generator=g, dtype=torch.int32).to(DEV)
+    gl = np.cumsum(counts).tolist()
+    y1, ys1 = cb.grouped_matmul_swiglu_quant_gather(x, idx, w, ws, xs, gl)
+    y2, ys2 = cb.grouped_matmul_swiglu_quant(x[idx.long()], w, ws, xs[idx.long()], gl)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2), "gathered int8 output differs from the explicit gather"
+    assert torch.equal(ys1, ys2), "gathered scales differ from the explicit gather"
+
+
+@pytest.mark.parametrize("counts,K,N", [([3, 5, 16], 512, 4096), ([100, 300], 256, 1024)])
+def test_gmsq_gather_out_of_range_rows(cb, counts, K, N):
+    """Indices outside [0, T) read a zero row with scale 0 (y = 0, y_scale = FLT_MIN / 127), the
+    same as the explicit operator on such a row; the other rows are unaffected."""
+    T = 40
+    g = cpu_gen(7 + K)
+    E, M = len(counts), sum(counts)
+    x = rand_i8((T, K), g)
+    w = rand_i8((E, K, N), g)
+    ws = (torch.rand(E, N, generator=g) * 0.009 + 0.001).to(DEV)
+    xs = (torch.rand(T, generator=g) * 0.015 + 0.005).to(DEV)
+    idx = torch.randint(0, T, (M,), generator=g, dtype=torch.int32)
+    idx[1] = -1
+    idx[M // 2] = T
+    idx[M - 1] = 1 << 30
+    gl = np.cumsum(counts).tolist()
+    y1, ys1 = cb.grouped_matmul_swiglu_quant_gather(x, idx.to(DEV), w, ws, xs, gl)
+    xe = torch.cat([x, torch.zeros(1, K, dtype=torch.int8, device=DEV)])
+    xse = torch.cat([xs, torch.zeros(1, device=DEV)])
+    ie = torch.where((idx >= 0) & (idx < T), idx, torch.full_like(idx, T)).long().to(DEV)
+    y2, ys2 = cb.grouped_matmul_swiglu_quant(xe[ie], w, ws, xse[ie], gl)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2) and torch.equal(ys1, ys2)
+    fm = np.float32(1.1754944e-38) * np.float32(1 / 127)
+    for r in (1, M // 2, M - 1):
+        assert (y1[r] == 0).all() and ys1[r].item() == fm
