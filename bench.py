@@ -127,6 +127,28 @@ def bench_prefill_gather(steps, warmup, dev, keep):
                        "K": K, "N": N, "row_index": "uniform random source token per routed row (torch seed 21), ascending within each expert"}}
 
 
+def bench_down_prefill(steps, warmup, dev, keep):
+    """The int8 grouped down-projection at the prefill size (context, not a BASELINE config): the GMSQ
+    prefill output shape x int8 [131072, 2048] (seeded random) over the prefill Zipf routing, weights
+    int8 [256, 2048, 7168], bf16 out [131072, 7168]."""
+    d = keep["prefill"]
+    M = d["x"].shape[0]
+    x = cfgs.rand_i8((M, 2048), dev, 41)
+    xs = cfgs.rand_uniform((M,), 0.005, 0.02, dev, 42)
+    w = cfgs.rand_i8((256, 2048, 7168), dev, 43)
+    ws = cfgs.rand_uniform((256, 7168), 0.001, 0.01, dev, 44)
+    ops = 2.0 * M * 2048 * 7168
+    fn = lambda: cb.grouped_matmul_quant(x, w, ws, xs, d["group_list"])
+    timer = KernelTimer(steps)
+    ms = time_op(fn, steps, warmup, timer)
+    kms = timer.mean_ms()
+    del x, w
+    return {"value": round(ops / (ms * 1e-3) / 1e12, 2), "unit": "TOPS", "ms_per_step": round(ms, 4),
+            "gemm_kernel_ms": round(kms, 4), "roofline": roofline("mfma", ops / (kms * 1e-3) / 1e12, "TFLOP/s"),
+            "config": {"workload": "down_proj_prefill", "rows": M, "K": 2048, "N": 7168, "experts": 256,
+                       "routing": "prefill zipf(1.1)"}}
+
+
 def decode_bytes(counts, K, N):
     M = int(np.sum(counts))
     act = int(np.sum(np.asarray(counts) > 0))
@@ -343,8 +365,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", default="prefill,gather,decode,ardq,qmm,routing,vendor",
-                    help="comma list of prefill, gather (needs prefill), decode, ardq, qmm, routing, vendor, copy")
+    ap.add_argument("--only", default="prefill,gather,down_prefill,decode,ardq,qmm,routing,vendor",
+                    help="comma list of prefill, gather and down_prefill (need prefill), decode, ardq, qmm, "
+                         "routing, vendor, copy")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -370,6 +393,8 @@ def main():
         out["frac_of_int8_peak"] = round(p["tops"] / PEAK_INT8_TOPS, 4)
         if "gather" in only:
             out["prefill_gather"] = bench_prefill_gather(args.steps, args.warmup, dev, keep)
+        if "down_prefill" in only:
+            out["down_proj_prefill"] = bench_down_prefill(args.steps, args.warmup, dev, keep)
     if "decode" in only:
         keep.pop("prefill_tensors", None)
         dres, down = bench_decode(args.steps, args.warmup, dev, keep)

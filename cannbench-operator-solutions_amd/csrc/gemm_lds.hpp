@@ -71,7 +71,7 @@ __device__ __forceinline__ void wait_vmcnt_barrier()
 
 template <int WM, int WN, int STAGES, int BK_ = 64>
 struct LdsCfg {
-    static constexpr int BM = 256, BN = 256, BK = BK_;
+    static constexpr int BM = 256, BN = 256, BK = BK_, STAGES_ = STAGES;
     static constexpr int KS = BK / 32;    // 32-deep MFMA steps per stage
     static constexpr int ACH = BK / 16;   // 16-byte chunks per A row
     static_assert(BK == 64 || BK == 128, "stage depth");
@@ -90,6 +90,86 @@ struct LdsCfg {
     static_assert(FN >= 2 && FN % 2 == 0, "wave tile must hold gate/up pairs");
 };
 
+// Global -> LDS DMA plan of one tile: the A and B buffer resources and each lane's stage-independent
+// source offsets.  A swizzle key: spreads the 16 rows of a ds_read_b128 phase over all 64 banks
+// (BK 64: 4 rows per 256 bytes, key (r >> 2) & 3; BK 128: 2 rows per 256 bytes, key (r >> 1) & 7).
+template <int ACH>
+__device__ __forceinline__ int a_swizzle(int r) { return ACH == 4 ? ((r >> 2) & 3) : ((r >> 1) & 7); }
+
+template <class C, bool SW>
+struct TileDma {
+    __amdgpu_buffer_rsrc_t ares, bres;
+    uint32_t a_off[C::A_ISSUE], b_off[C::B_ISSUE];
+    uint32_t n;  // weight row length
+    int nk;
+
+    __device__ __forceinline__ void init(const GemmArgs& a, const int mt, const int nt, const int64_t b, const int wave,
+                                         const int lane)
+    {
+        constexpr int BM = C::BM, BN = C::BN, NW = C::NW, ACH = C::ACH;
+        const int64_t K = a.K, N = a.N;
+        const int g = group_of_tile(a.gt, mt);
+        const int rs = g ? a.gt.row_end[g - 1] : 0;
+        const int m0 = rs + (mt - a.gt.tile_start[g]) * BM;
+        const int vrows = a.gt.row_end[g] - m0;
+        // A = rows [m0, r1) of x (with a row index: all of x, rows gathered through the per-lane
+        // offsets), B = this group's weight [K, N]
+        const bool gather = a.row_index != nullptr;
+        ares = gather ? make_rsrc(a.x, (uint32_t)(a.x_rows * K))
+                      : make_rsrc(a.x + b * a.x_bstride + (int64_t)m0 * K, (uint32_t)((int64_t)vrows * K));
+        bres = make_rsrc(a.w + b * a.w_bstride + (int64_t)g * a.w_gstride, (uint32_t)(K * N));
+        n = (uint32_t)N;
+        nk = (int)((K + C::BK - 1) / C::BK);
+#pragma unroll
+        for (int i = 0; i < C::A_ISSUE; ++i) {
+            const int cid = (i * NW + wave) * 64 + lane;  // 16-byte chunk id in the A tile
+            const int row = cid / ACH, pos = cid % ACH;
+            const int q = pos ^ a_swizzle<ACH>(row);
+            // rows past the tile's valid rows (and gathered rows outside x) point past the resource:
+            // they read zeros and fetch nothing, so a partial tile moves only its valid rows
+            const int srow = row < vrows ? (gather ? src_row(a, m0 + row) : row) : -1;
+            a_off[i] = srow >= 0 ? (uint32_t)srow * (uint32_t)K + (uint32_t)(q * 16) : 0x80000000u;
+        }
+#pragma unroll
+        for (int i = 0; i < C::B_ISSUE; ++i) {
+            const int cid = (i * NW + wave) * 64 + lane;
+            const int row = cid >> 4, pos = cid & 15;
+            const int c = pos ^ ((row & 7) << 1);  // logical 16-column chunk
+            int64_t col;
+            bool ok;
+            if constexpr (SW) {
+                const int64_t j = (int64_t)nt * (BN / 2) + 16 * (c & 7);
+                ok = j < a.epi.H;
+                col = c < 8 ? j : a.epi.H + j;
+            } else {
+                col = (int64_t)nt * BN + 16 * c;
+                ok = col < N;
+            }
+            b_off[i] = (uint32_t)row * (uint32_t)N + (uint32_t)(ok ? col : 0);
+        }
+    }
+
+    // DMAs of stage kt into ring slot kt % STAGES.  Stages past K keep the DMA count (and so every
+    // wait) constant but fetch nothing: weight offsets past K*N already lie outside their resource,
+    // activation offsets would run into the next rows, so they are moved outside the resource too.
+    __device__ __forceinline__ void issue(const int kt, const uint32_t lds_base, const int wave) const
+    {
+        constexpr int NW = C::NW;
+        const uint32_t sa = lds_base + (uint32_t)((kt % C::STAGES_) * C::STAGE);
+        const uint32_t sb = sa + C::A_BYTES;
+        const uint32_t ka = (uint32_t)(kt * C::BK);
+        const uint32_t kb = (uint32_t)(kt * C::BK) * n;
+        const bool live = kt < nk;
+#pragma unroll
+        for (int i = 0; i < C::A_ISSUE; ++i)
+            dma16(ares, live ? a_off[i] + ka : 0x80000000u,
+                  __builtin_amdgcn_readfirstlane(sa + (uint32_t)((i * NW + wave) * 1024)));
+#pragma unroll
+        for (int i = 0; i < C::B_ISSUE; ++i)
+            dma16(bres, b_off[i] + kb, __builtin_amdgcn_readfirstlane(sb + (uint32_t)((i * NW + wave) * 1024)));
+    }
+};
+
 // One 256 x 256 output tile (row tile mt, column tile nt, batch b).  Called once per workgroup by
 // lds_gemm_kernel and in a loop by the persistent fused-requant kernel.
 template <int EPI, int WM, int WN, int STAGES, int BKT>
@@ -99,9 +179,6 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
     using C = LdsCfg<WM, WN, STAGES, BKT>;
     constexpr bool SW = EPI == EPI_SWIGLU || EPI == EPI_SWIGLU_Q;
     constexpr int KS = C::KS, ACH = C::ACH;
-    // A swizzle key: spreads the 16 rows of a ds_read_b128 phase over all 64 banks
-    // (BK 64: 4 rows per 256 bytes, key (r >> 2) & 3; BK 128: 2 rows per 256 bytes, key (r >> 1) & 7)
-    auto a_swz = [](int r) { return ACH == 4 ? ((r >> 2) & 3) : ((r >> 1) & 7); };
     constexpr int BM = C::BM, BN = C::BN, BK = C::BK, NW = C::NW, TN = C::TN, FM = C::FM,
                   FN = C::FN;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -116,60 +193,11 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
     const int m0 = rs + (mt - a.gt.tile_start[g]) * BM;
     const int vrows = r1 - m0;  // valid rows of this tile (>= 1)
 
-    // buffer resources: A = rows [m0, r1) of x (with a row index: all of x, rows gathered through
-    // the per-lane DMA offsets), B = this group's weight [K, N]
-    const bool gather = a.row_index != nullptr;
-    const __amdgpu_buffer_rsrc_t ares =
-        gather ? make_rsrc(a.x, (uint32_t)(a.x_rows * K))
-               : make_rsrc(a.x + b * a.x_bstride + (int64_t)m0 * K, (uint32_t)((int64_t)vrows * K));
-    const __amdgpu_buffer_rsrc_t bres =
-        make_rsrc(a.w + b * a.w_bstride + (int64_t)g * a.w_gstride, (uint32_t)(K * N));
-
-    // ---- per-lane DMA source offsets (stage independent part) -----------------------------
-    uint32_t a_off[C::A_ISSUE];
-#pragma unroll
-    for (int i = 0; i < C::A_ISSUE; ++i) {
-        const int cid = (i * NW + wave) * 64 + lane;  // 16-byte chunk id in the A tile
-        const int row = cid / ACH, pos = cid % ACH;
-        const int q = pos ^ a_swz(row);
-        // rows past the tile's valid rows (and gathered rows outside x) point past the resource:
-        // they read zeros and fetch nothing, so a partial tile moves only its valid rows
-        const int srow = row < vrows ? (gather ? src_row(a, m0 + row) : row) : -1;
-        a_off[i] = srow >= 0 ? (uint32_t)srow * (uint32_t)K + (uint32_t)(q * 16) : 0x80000000u;
-    }
-    uint32_t b_off[C::B_ISSUE];
-#pragma unroll
-    for (int i = 0; i < C::B_ISSUE; ++i) {
-        const int cid = (i * NW + wave) * 64 + lane;
-        const int row = cid >> 4, pos = cid & 15;
-        const int c = pos ^ ((row & 7) << 1);  // logical 16-column chunk
-        int64_t col;
-        bool ok;
-        if constexpr (SW) {
-            const int64_t j = (int64_t)nt * (BN / 2) + 16 * (c & 7);
-            ok = j < e.H;
-            col = c < 8 ? j : e.H + j;
-        } else {
-            col = (int64_t)nt * BN + 16 * c;
-            ok = col < N;
-        }
-        b_off[i] = (uint32_t)row * (uint32_t)N + (uint32_t)(ok ? col : 0);
-    }
-
+    TileDma<C, SW> dma;
+    dma.init(a, mt, nt, b, wave, lane);
     const uint32_t lds_base = (uint32_t)(uintptr_t)(CB_LDS uint8_t*)smem;
-    const int nk = (int)((K + BK - 1) / BK);
-    auto issue_stage = [&](int kt) {
-        const uint32_t sa = lds_base + (uint32_t)((kt % STAGES) * C::STAGE);
-        const uint32_t sb = sa + C::A_BYTES;
-        const uint32_t ka = (uint32_t)(kt * BK);
-        const uint32_t kb = (uint32_t)(kt * BK) * (uint32_t)N;
-#pragma unroll
-        for (int i = 0; i < C::A_ISSUE; ++i)
-            dma16(ares, a_off[i] + ka, __builtin_amdgcn_readfirstlane(sa + (uint32_t)((i * NW + wave) * 1024)));
-#pragma unroll
-        for (int i = 0; i < C::B_ISSUE; ++i)
-            dma16(bres, b_off[i] + kb, __builtin_amdgcn_readfirstlane(sb + (uint32_t)((i * NW + wave) * 1024)));
-    };
+    const int nk = dma.nk;
+    auto issue_stage = [&](int kt) { dma.issue(kt, lds_base, wave); };
 
     auto tcol = [&](int fn) -> int {  // first tile column of wave fragment fn
         if constexpr (SW)
@@ -189,7 +217,7 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             const int q = 2 * ks + (lane >> 5);
-            a_rd[fm][ks] = (uint32_t)(r * BK + ((q ^ a_swz(r)) << 4));
+            a_rd[fm][ks] = (uint32_t)(r * BK + ((q ^ a_swizzle<ACH>(r)) << 4));
         }
     }
     // B: group gq = lane / 16 -> k half (gq >> 1), column half (gq & 1); in-group lane s -> row
