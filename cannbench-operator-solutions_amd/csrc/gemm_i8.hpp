@@ -37,7 +37,7 @@ enum { BIAS_NONE = 0, BIAS_I32 = 1, BIAS_F16 = 2, BIAS_BF16 = 3, BIAS_F32 = 4 };
 // EPI_DEQUANT computes, like the reference QuantMatmul epilogue
 // (quant_matmul_epilogue_kernel.cpp:15-22, 261-305):
 //   v = float(c); [v += bias (int32 kind)]; v *= scale[n]; [v += offset[n]];
-//   [v *= pertoken[row % pt_mod]]; [v += bias (float kinds)]; out = round16(v)
+//   [v *= pertoken[row]]; [v += bias (float kinds)]; out = round16(v)
 // scale may be offset per group (scale_gstride elements) for the grouped down-projection.
 //
 // EPI_SWIGLU computes, like the reference GMSQ vector stage (gmsq_vec_kernel.cpp:15-20, 207-231):
@@ -53,7 +53,6 @@ struct EpiArgs {
     int32_t has_offset;
     int32_t offset_perchan;
     const float* pertoken;
-    int64_t pt_mod;
     int32_t has_pt;
     int32_t bias_kind;
     const void* bias;
@@ -402,7 +401,7 @@ __global__ __launch_bounds__(256, PREFETCH ? 2 : CB_SKINNY_OCC) void skinny_kern
             }
         } else {
             if (rowok && colok) {
-                const float pt = e.has_pt ? e.pertoken[row % e.pt_mod] : 1.0f;
+                const float pt = e.has_pt ? e.pertoken[row] : 1.0f;
                 const int64_t oc = opaque(ocol);
                 u32 packed[8];
 #pragma unroll
@@ -686,7 +685,7 @@ __global__ __launch_bounds__(256, 1) void tiled_kernel(const GemmArgs a)
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm * TM + fm * 32 + (r >> 2) * 8 + lr + (r & 3);
                 if (row >= r1) continue;
-                const float pt = e.has_pt ? e.pertoken[row % e.pt_mod] : 1.0f;
+                const float pt = e.has_pt ? e.pertoken[row] : 1.0f;
 #pragma unroll
                 for (int fn = 0; fn < FN; ++fn) {
                     if (cok[fn]) {
@@ -753,7 +752,7 @@ __global__ __launch_bounds__(256) void generic_dequant_kernel(const GemmArgs a)
     for (int64_t k = 0; k < a.K; ++k) acc += (int)xr[k] * (int)wg[k * a.N + col];
     const EpiArgs& e = a.epi;
     const ColDeq d = col_deq(e, g, b, col);
-    const float pt = e.has_pt ? e.pertoken[row % e.pt_mod] : 1.0f;
+    const float pt = e.has_pt ? e.pertoken[row] : 1.0f;
     const float v = apply_deq(e, d, acc, pt);
     uint16_t* ob = (uint16_t*)e.out + b * e.out_bstride;
     ob[(int64_t)row * a.N + col] = e.out_bf16 ? f32_to_bf16(v) : f32_to_f16(v);

@@ -546,23 +546,39 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
         }
         epi_barrier();
         CB_LDS uint8_t* st = (CB_LDS uint8_t*)smem;
+        // The flags are uniform: branch once per tile rather than per value, so the common chain
+        // (per-channel scale, optional pertoken, no offset or bias, bf16 out: QuantMatmul and the
+        // down-projection) runs without the selects of every other variant.  Its arithmetic is
+        // apply_deq's for those flags (v * 1.0f when there is no pertoken scale is exact).
+        auto stage = [&](auto simple_const) {
+            constexpr bool SIMPLE = decltype(simple_const)::value;
 #pragma unroll
-        for (int fm = 0; fm < FM; ++fm) {
-            if (!fvalid[fm]) continue;
+            for (int fm = 0; fm < FM; ++fm) {
+                if (!fvalid[fm]) continue;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int lrow = (WM * fm + wm) * 32 + (r >> 2) * 8 + lr + (r & 3);
-                const int row = m0 + lrow < r1 ? m0 + lrow : r1 - 1;
-                const float pt = e.has_pt ? e.pertoken[row % e.pt_mod] : 1.0f;
+                for (int r = 0; r < 16; ++r) {
+                    const int lrow = (WM * fm + wm) * 32 + (r >> 2) * 8 + lr + (r & 3);
+                    const int row = m0 + lrow < r1 ? m0 + lrow : r1 - 1;
+                    const float pt = e.has_pt ? e.pertoken[row] : 1.0f;
 #pragma unroll
-                for (int fn = 0; fn < FN; ++fn) {
-                    const float v = apply_deq(e, cd[fn], acc[fm][fn][r], pt);
-                    const uint16_t h = e.out_bf16 ? f32_to_bf16_hw(v) : f32_to_f16(v);
-                    const int lcol = wn * TN + fn * 32 + (lane & 31);
-                    *(CB_LDS uint16_t*)(st + lrow * C::EPI_PITCH + lcol * 2) = h;
+                    for (int fn = 0; fn < FN; ++fn) {
+                        uint16_t h;
+                        if constexpr (SIMPLE) {
+                            h = f32_to_bf16_hw(((float)acc[fm][fn][r] * cd[fn].scale) * pt);
+                        } else {
+                            const float v = apply_deq(e, cd[fn], acc[fm][fn][r], pt);
+                            h = e.out_bf16 ? f32_to_bf16_hw(v) : f32_to_f16(v);
+                        }
+                        const int lcol = wn * TN + fn * 32 + (lane & 31);
+                        *(CB_LDS uint16_t*)(st + lrow * C::EPI_PITCH + lcol * 2) = h;
+                    }
                 }
             }
-        }
+        };
+        if (!e.has_offset && e.bias_kind == BIAS_NONE && e.out_bf16)
+            stage(std::integral_constant<bool, true>());
+        else
+            stage(std::integral_constant<bool, false>());
         epi_barrier();
         uint16_t* ob = (uint16_t*)e.out + b * e.out_bstride;
         constexpr int CHUNKS = BM * (BN * 2 / 16);  // 16-byte chunks in the tile

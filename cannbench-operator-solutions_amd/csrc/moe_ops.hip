@@ -368,7 +368,6 @@ extern "C" int cb_grouped_matmul_quant(const int8_t* x, const int8_t* weight, co
     a.epi.scale_perchan = 1;
     a.epi.pertoken = x_scale;
     a.epi.has_pt = 1;
-    a.epi.pt_mod = M;
     a.epi.out = out;
     a.epi.out_bf16 = 1;
     const bool fast = K > 0 && K % 16 == 0 && N % 16 == 0 && aligned(x, 16) && aligned(weight, 16) &&
@@ -435,7 +434,6 @@ extern "C" int cb_quant_matmul(const int8_t* x1, const int8_t* x2, const void* s
     e.offset_perchan = offset_numel > 1;
     e.pertoken = pertoken;
     e.has_pt = pertoken_numel != 0;
-    e.pt_mod = M;
     e.bias = bias;
     e.bias_kind = bias_kind;
     e.bias_perchan = bias_batched ? (N > 1) : (bias_numel > 1);
