@@ -149,13 +149,34 @@ struct TileDma {
         }
     }
 
-    // DMAs of stage kt into ring slot kt % STAGES.  Stages past K keep the DMA count (and so every
-    // wait) constant but fetch nothing: weight offsets past K*N already lie outside their resource,
-    // activation offsets would run into the next rows, so they are moved outside the resource too.
+    // A plan that fetches nothing (every offset lies outside an empty resource): the stage stream
+    // of a persistent workgroup past its last tile.
+    __device__ __forceinline__ void set_dead(const GemmArgs& a)
+    {
+        ares = make_rsrc(a.x, 0u);
+        bres = make_rsrc(a.w, 0u);
+#pragma unroll
+        for (int i = 0; i < C::A_ISSUE; ++i) a_off[i] = 0x80000000u;
+#pragma unroll
+        for (int i = 0; i < C::B_ISSUE; ++i) b_off[i] = 0x80000000u;
+        n = 0;
+        nk = 0;
+    }
+
+    // DMAs of stage kt into ring slot kt % STAGES.
     __device__ __forceinline__ void issue(const int kt, const uint32_t lds_base, const int wave) const
     {
+        issue_at(kt, kt % C::STAGES_, lds_base, wave);
+    }
+
+    // DMAs of stage kt into ring slot `slot`.  Stages past K keep the DMA count (and so every
+    // wait) constant but fetch nothing: weight offsets past K*N already lie outside their resource,
+    // activation offsets would run into the next rows, so they are moved outside the resource too.
+    __device__ __forceinline__ void issue_at(const int kt, const int slot, const uint32_t lds_base,
+                                             const int wave) const
+    {
         constexpr int NW = C::NW;
-        const uint32_t sa = lds_base + (uint32_t)((kt % C::STAGES_) * C::STAGE);
+        const uint32_t sa = lds_base + (uint32_t)(slot * C::STAGE);
         const uint32_t sb = sa + C::A_BYTES;
         const uint32_t ka = (uint32_t)(kt * C::BK);
         const uint32_t kb = (uint32_t)(kt * C::BK) * n;
@@ -170,21 +191,32 @@ struct TileDma {
     }
 };
 
-// One 256 x 256 output tile (row tile mt, column tile nt, batch b).  Called once per workgroup by
-// lds_gemm_kernel and in a loop by the persistent fused-requant kernel.
 template <int EPI, int WM, int WN, int STAGES, int BKT>
+using TileDmaOf = TileDma<LdsCfg<WM, WN, STAGES, BKT>, EPI == EPI_SWIGLU || EPI == EPI_SWIGLU_Q>;
+
+// One 256 x 256 output tile (row tile mt, column tile nt, batch b).  Called once per workgroup by
+// lds_gemm_kernel and in a loop by the persistent kernels.
+//
+// CONT (continuous stage stream, persistent dequant / int32 kernel): the tile's first STAGES stages
+// were already issued by the previous tile (or the kernel's prologue) from the plan `cur` into ring
+// slots sbase, sbase + 1, ...; the last STAGES iterations of this tile issue the first stages of
+// the plan `nxt`.  The epilogue then writes from registers and leaves the LDS ring to those DMAs.
+template <int EPI, int WM, int WN, int STAGES, int BKT, bool CONT = false>
 __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, const int nt, const int64_t b,
-                                              uint8_t* smem, const int arr_idx = 0, const u32 arr_target = 0)
+                                              uint8_t* smem, const int arr_idx = 0, const u32 arr_target = 0,
+                                              const TileDmaOf<EPI, WM, WN, STAGES, BKT>* cur = nullptr,
+                                              const TileDmaOf<EPI, WM, WN, STAGES, BKT>* nxt = nullptr,
+                                              const int sbase = 0)
 {
     using C = LdsCfg<WM, WN, STAGES, BKT>;
     constexpr bool SW = EPI == EPI_SWIGLU || EPI == EPI_SWIGLU_Q;
     constexpr int KS = C::KS, ACH = C::ACH;
-    constexpr int BM = C::BM, BN = C::BN, BK = C::BK, NW = C::NW, TN = C::TN, FM = C::FM,
+    constexpr int BM = C::BM, BN = C::BN, BK = C::BK, TN = C::TN, FM = C::FM,
                   FN = C::FN;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
-    const int64_t K = a.K, N = a.N;
+    const int64_t N = a.N;
     const EpiArgs& e = a.epi;
 
     const int g = group_of_tile(a.gt, mt);
@@ -193,11 +225,23 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
     const int m0 = rs + (mt - a.gt.tile_start[g]) * BM;
     const int vrows = r1 - m0;  // valid rows of this tile (>= 1)
 
+    static_assert(!(CONT && SW), "continuous stage stream: dequant / int32 epilogues only");
     TileDma<C, SW> dma;
-    dma.init(a, mt, nt, b, wave, lane);
+    if constexpr (CONT) dma = *cur;
+    else dma.init(a, mt, nt, b, wave, lane);
     const uint32_t lds_base = (uint32_t)(uintptr_t)(CB_LDS uint8_t*)smem;
     const int nk = dma.nk;
-    auto issue_stage = [&](int kt) { dma.issue(kt, lds_base, wave); };
+    auto slot_of = [&](int kt) { return CONT ? (sbase + kt) % STAGES : kt % STAGES; };
+    auto issue_stage = [&](int kt) {
+        if constexpr (CONT) {
+            // uniform branch right after a barrier that drained lgkmcnt: nothing for the compiler
+            // to wait on at the join
+            if (kt < nk) dma.issue_at(kt, slot_of(kt), lds_base, wave);
+            else nxt->issue_at(kt - nk, slot_of(kt), lds_base, wave);
+        } else {
+            dma.issue(kt, lds_base, wave);
+        }
+    };
 
     auto tcol = [&](int fn) -> int {  // first tile column of wave fragment fn
         if constexpr (SW)
@@ -221,22 +265,19 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
         }
     }
     // B: group gq = lane / 16 -> k half (gq >> 1), column half (gq & 1); in-group lane s -> row
-    // offset s >> 1, byte half s & 1
+    // offset s >> 1, byte half s & 1.  The read of (fn, ks, hf) covers stage row
+    // ks * 32 + (gq >> 1) * 16 + hf * 8 + (s >> 1), whose swizzle key (row & 7) = s >> 1 does not
+    // depend on ks or hf: one base offset per fragment, the rest are instruction immediates.
     const int gq = lane >> 4, s = lane & 15;
-    uint32_t b_rd[FN][KS][2];  // [fn][ks][low/high 8 k]
+    uint32_t b_rd[FN];
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) {
         const int cc = (tcol(fn) >> 4) + (gq & 1);
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                const int row = ks * 32 + (gq >> 1) * 16 + hf * 8 + (s >> 1);
-                const int pos = cc ^ ((row & 7) << 1);
-                b_rd[fn][ks][hf] = (uint32_t)(C::A_BYTES + row * BN + pos * 16 + (s & 1) * 8);
-            }
-        }
+        const int row = (gq >> 1) * 16 + (s >> 1);
+        const int pos = cc ^ ((s >> 1) << 1);
+        b_rd[fn] = (uint32_t)(C::A_BYTES + row * BN + pos * 16 + (s & 1) * 8);
     }
+    auto b_rd_at = [&](int fn, int ks, int hf) -> uint32_t { return b_rd[fn] + (uint32_t)((ks * 32 + hf * 8) * BN); };
 
     // 32-row fragments of this wave that hold valid rows (wave-uniform); tiles at a group's end run
     // a loop variant without the MFMAs of the empty fragments
@@ -255,8 +296,10 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
     // iteration unconditionally, so the number of DMAs in flight is always the same and every
     // wait is a compile-time constant; stages past the end of K only fetch zeros or unused bytes
     // into buffers that are never read again.
+    if constexpr (!CONT) {
 #pragma unroll
-    for (int st = 0; st < STAGES; ++st) issue_stage(st);
+        for (int st = 0; st < STAGES; ++st) issue_stage(st);
+    }
 
     // Software pipeline per stage kt (fragments of half-stage ks = 0 already in registers):
     //   read ks = 1 fragments | MFMAs on ks = 0 | barrier for stage kt + 1, refill the buffer
@@ -270,14 +313,14 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
         v4i a0[NVA], b0[FN], a1[NVA], b1[FN];
         auto load = [&](int kt, int ks, v4i (&af)[NVA], v4i (&bf)[FN]) {
             if constexpr (NV > 0) {
-                const CB_LDS uint8_t* base = (const CB_LDS uint8_t*)smem + (kt % STAGES) * C::STAGE;
+                const CB_LDS uint8_t* base = (const CB_LDS uint8_t*)smem + slot_of(kt) * C::STAGE;
 #ifndef CB_ABLATE_NO_LDSREAD
 #pragma unroll
                 for (int fm = 0; fm < NV; ++fm) af[fm] = *(const CB_LDS v4i*)(base + a_rd[fm][ks]);
 #pragma unroll
                 for (int fn = 0; fn < FN; ++fn) {
-                    const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((CB_LDS v2i*)(base + b_rd[fn][ks][0]));
-                    const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((CB_LDS v2i*)(base + b_rd[fn][ks][1]));
+                    const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((CB_LDS v2i*)(base + b_rd_at(fn, ks, 0)));
+                    const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((CB_LDS v2i*)(base + b_rd_at(fn, ks, 1)));
                     bf[fn] = v4i{lo[0], lo[1], hi[0], hi[1]};
                 }
 #else
@@ -397,7 +440,98 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
 #endif
     // ---- epilogue.  32x32 C layout: lane l holds column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4
     const int lr = (lane >> 5) * 4;
-    if constexpr (SW) {
+    if constexpr (CONT) {
+        // Register-direct epilogue (the LDS ring already receives the next tile's stages).  Stores
+        // go through a resource over this tile's valid rows: rows past the group, including whole
+        // fragments without valid rows (their accumulators stayed zero), are dropped, so there is
+        // no branch whose join would make the compiler wait for the stores issued before it.
+        // Column offsets of fragment fn: col0 + 32 fn, outside the resource past N.
+        const int64_t col0 = (int64_t)nt * BN + wn * TN + (lane & 31);
+        if constexpr (EPI == EPI_I32) {
+            const __amdgpu_buffer_rsrc_t ores =
+                make_rsrc((int32_t*)e.out + b * e.out_bstride + (int64_t)m0 * N, (uint32_t)(vrows * N * 4));
+            uint32_t coff[FN];
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn) coff[fn] = col0 + 32 * fn < N ? (uint32_t)(col0 + 32 * fn) * 4u : 0x80000000u;
+#pragma unroll
+            for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int lrow = (WM * fm + wm) * 32 + (r >> 2) * 8 + lr + (r & 3);
+                    const uint32_t roff = (uint32_t)lrow * (uint32_t)N * 4u;
+#pragma unroll
+                    for (int fn = 0; fn < FN; ++fn)
+                        __builtin_amdgcn_raw_buffer_store_b32(acc[fm][fn][r], ores, roff + coff[fn], 0, 0);
+                }
+            }
+        } else {
+            // Rows r and r + 1 of a lane pair (l, l ^ 1) are swapped so that each lane stores two
+            // adjacent columns of one row as one dword: the even lane row r, columns (c, c + 1),
+            // the odd lane row r + 1, columns (c - 1, c).
+            const __amdgpu_buffer_rsrc_t ores =
+                make_rsrc((uint16_t*)e.out + b * e.out_bstride + (int64_t)m0 * N, (uint32_t)(vrows * N * 2));
+            const bool odd = lane & 1;
+            ColDeq cd[FN];
+            uint32_t coff[FN];
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn) {
+                const int64_t cc = col0 + 32 * fn;
+                cd[fn] = col_deq(e, g, b, cc < N ? cc : 0);
+                coff[fn] = cc < N ? (uint32_t)(cc & ~(int64_t)1) * 2u : 0x80000000u;
+            }
+            // Every row scale is loaded before the first store: a load between stores would make
+            // its wait (vmcnt counts stores too) drain the stores issued before it.
+            float ptv[FM][16];
+            if (e.has_pt) {
+#pragma unroll
+                for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int lrow = (WM * fm + wm) * 32 + (r >> 2) * 8 + lr + (r & 3);
+                        ptv[fm][r] = e.pertoken[m0 + lrow < r1 ? m0 + lrow : r1 - 1];
+                    }
+            } else {
+#pragma unroll
+                for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) ptv[fm][r] = 1.0f;
+            }
+            auto store = [&](auto simple_const) {
+                constexpr bool SIMPLE = decltype(simple_const)::value;
+#pragma unroll
+                for (int fm = 0; fm < FM; ++fm) {
+    #pragma unroll
+                    for (int r = 0; r < 16; r += 2) {
+                        const int lrow = (WM * fm + wm) * 32 + (r >> 2) * 8 + lr + (r & 3);  // rows lrow, lrow + 1
+                        const float pt0 = ptv[fm][r], pt1 = ptv[fm][r + 1];
+                        const uint32_t roff = (uint32_t)(lrow + (odd ? 1 : 0)) * (uint32_t)N * 2u;
+#pragma unroll
+                        for (int fn = 0; fn < FN; ++fn) {
+                            uint32_t h0, h1;
+                            if constexpr (SIMPLE) {
+                                h0 = f32_to_bf16_hw(((float)acc[fm][fn][r] * cd[fn].scale) * pt0);
+                                h1 = f32_to_bf16_hw(((float)acc[fm][fn][r + 1] * cd[fn].scale) * pt1);
+                            } else {
+                                const float v0 = apply_deq(e, cd[fn], acc[fm][fn][r], pt0);
+                                const float v1 = apply_deq(e, cd[fn], acc[fm][fn][r + 1], pt1);
+                                h0 = e.out_bf16 ? f32_to_bf16_hw(v0) : f32_to_f16(v0);
+                                h1 = e.out_bf16 ? f32_to_bf16_hw(v1) : f32_to_f16(v1);
+                            }
+                            const uint32_t p = h0 | (h1 << 16);
+                            // partner lane's pair (quad_perm [1, 0, 3, 2])
+                            const uint32_t q = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)p, 0xB1, 0xF, 0xF, false);
+                            const uint32_t w = odd ? ((q >> 16) | (p & 0xffff0000u)) : ((p & 0xffffu) | (q << 16));
+                            __builtin_amdgcn_raw_buffer_store_b32(w, ores, roff + coff[fn], 0, 0);
+                        }
+                    }
+                }
+            };
+            if (!e.has_offset && e.bias_kind == BIAS_NONE && e.out_bf16)
+                store(std::integral_constant<bool, true>());
+            else
+                store(std::integral_constant<bool, false>());
+        }
+    } else if constexpr (SW) {
         // act tile [256 rows][128 act columns] fp32 staged in LDS, then written with 16-byte stores
         // and one row-max atomic per (row, tile)
         const int64_t H = e.H;
@@ -595,6 +729,23 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
     }
 }
 
+// Tile pid of the non-persistent launch order: GROUP_M row tiles x all column tiles per group of
+// pids, so the workgroups resident together share GROUP_M activation slabs and their weights.
+#ifndef CB_GROUP_M
+#define CB_GROUP_M 4
+#endif
+__device__ __forceinline__ void tile_of_pid(const GemmArgs& a, const int pid, int& mt, int& nt)
+{
+    constexpr int GROUP_M = CB_GROUP_M;
+    const int T_m = a.gt.total_mtiles, T_n = a.ntiles;
+    const int per_group = GROUP_M * T_n;
+    const int gid = pid / per_group;
+    const int first_m = gid * GROUP_M;
+    const int gsz = (T_m - first_m) < GROUP_M ? (T_m - first_m) : GROUP_M;
+    mt = first_m + (pid % per_group) % gsz;
+    nt = (pid % per_group) / gsz;
+}
+
 // Non-persistent launch: one tile per workgroup.
 template <int EPI, int WM, int WN, int STAGES, int BKT>
 __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArgs a)
@@ -608,18 +759,51 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
 #else
     const int pid = blockIdx.x;
 #endif
-#ifndef CB_GROUP_M
-#define CB_GROUP_M 4
-#endif
-    constexpr int GROUP_M = CB_GROUP_M;
-    const int T_m = a.gt.total_mtiles, T_n = a.ntiles;
-    const int per_group = GROUP_M * T_n;
-    const int gid = pid / per_group;
-    const int first_m = gid * GROUP_M;
-    const int gsz = (T_m - first_m) < GROUP_M ? (T_m - first_m) : GROUP_M;
-    const int mt = first_m + (pid % per_group) % gsz;
-    const int nt = (pid % per_group) / gsz;
+    int mt, nt;
+    tile_of_pid(a, pid, mt, nt);
     lds_gemm_tile<EPI, WM, WN, STAGES, BKT>(a, mt, nt, blockIdx.y, smem);
+}
+
+// Persistent dequant / int32 GEMM (batch 1): gridDim.x workgroups, one per CU, walk the tiles
+// pid = blockIdx.x, blockIdx.x + gridDim.x, ... of the non-persistent order.  One continuous stage
+// stream per workgroup: a tile's last STAGES iterations DMA the next tile's first stages, so no tile
+// starts with an empty ring, and the register-direct epilogue overlaps those DMAs.
+template <int EPI, int WM, int WN, int STAGES, int BKT>
+__global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_persistent_kernel(const GemmArgs a)
+{
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    const int total = a.gt.total_mtiles * a.ntiles;
+    int pid = blockIdx.x;
+    if (pid >= total) return;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(CB_LDS uint8_t*)smem;
+    TileDmaOf<EPI, WM, WN, STAGES, BKT> cur, nxt;
+    int mt, nt;
+    tile_of_pid(a, pid, mt, nt);
+    cur.init(a, mt, nt, 0, wave, lane);
+#pragma unroll
+    for (int st = 0; st < STAGES; ++st) cur.issue_at(st, st, lds_base, wave);
+    int sbase = 0;
+    for (;;) {
+        const int pn = pid + (int)gridDim.x;
+        int mt2 = 0, nt2 = 0;
+        if (pn < total) {
+            tile_of_pid(a, pn, mt2, nt2);
+            nxt.init(a, mt2, nt2, 0, wave, lane);
+        } else {
+            nxt.set_dead(a);
+        }
+        lds_gemm_tile<EPI, WM, WN, STAGES, BKT, true>(a, mt, nt, 0, smem, 0, 0, &cur, &nxt, sbase);
+        if (pn >= total) break;
+        sbase = (sbase + cur.nk) % STAGES;
+        cur = nxt;
+        pid = pn;
+        mt = mt2;
+        nt = nt2;
+    }
+    // the dead stages issued by the last tile fetch nothing; drain them before the wave ends
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Persistent GroupedMatmulSwigluQuant with the requant fused.  gridDim.x workgroups, at most one per

@@ -5,6 +5,7 @@
 // plus the status strings.  Each entry point validates in the reference plugin's order, then
 // enqueues its kernels on the caller's stream without any allocation or host synchronisation.
 #include <cstring>
+#include <cstdlib>
 #include <mutex>
 #include <set>
 #include <utility>
@@ -91,6 +92,16 @@ static int device_cus()
     return cus[dev];
 }
 
+// Workgroups of the persistent dequant / int32 GEMM: one per CU.  CANNBENCH_AMD_PERSISTENT_GRID
+// overrides it (a small grid makes every workgroup walk many tiles: the parity tests use it);
+// a value <= 0 turns the persistent launch off.
+static int persistent_grid()
+{
+    const char* s = std::getenv("CANNBENCH_AMD_PERSISTENT_GRID");
+    if (s && *s) return std::atoi(s);
+    return device_cus();
+}
+
 // Raise a kernel's dynamic LDS limit once per (kernel, device): the attribute belongs to the
 // kernel as loaded on the current device, so a process driving several GPUs sets it on each.
 static void allow_dynamic_lds(const void* kern, int bytes)
@@ -128,7 +139,11 @@ static constexpr bool kSkinnyPrefetch = CB_SKINNY_PREFETCH;
 #ifndef CB_FUSED_REQUANT
 #define CB_FUSED_REQUANT 1
 #endif
+#ifndef CB_PERSISTENT_GEMM
+#define CB_PERSISTENT_GEMM 1
+#endif
 static constexpr bool kUseLdsCore = CB_LDS_CORE;
+static constexpr bool kPersistentGemm = CB_PERSISTENT_GEMM;
 static constexpr bool kFusedRequant = CB_FUSED_REQUANT;
 static constexpr int kLdsWM = CB_LDS_WM, kLdsWN = CB_LDS_WN, kLdsStages = CB_LDS_STAGES, kLdsBK = CB_LDS_BK;
 
@@ -174,6 +189,21 @@ static void launch_gemm(GemmArgs& a, const int64_t* gl, int64_t E, int64_t batch
         using Cfg = LdsCfg<kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
         build_group_table(a.gt, gl, E, Cfg::BM);
         const int64_t blocks = (int64_t)a.gt.total_mtiles * a.ntiles;
+        const int pg = persistent_grid();
+        // persistent launch once there are more tiles than workgroups (one continuous DMA stream
+        // per workgroup: a tile's last STAGES iterations issue the next tile's first STAGES
+        // stages, so K must span at least STAGES stages); its register-direct epilogue addresses
+        // a tile's rows with 32-bit offsets
+        if constexpr (kPersistentGemm && EPI != EPI_SWIGLU) {
+            if (batch == 1 && pg > 0 && blocks > pg && a.K >= (int64_t)Cfg::STAGES_ * Cfg::BK &&
+                Cfg::BM * Ncols * 4 < 0x7fffffffLL) {
+                auto kern = lds_gemm_persistent_kernel<EPI, kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
+                constexpr int lds = Cfg::STAGES_ * Cfg::STAGE;  // the ring: the epilogue needs no LDS
+                allow_dynamic_lds((const void*)kern, lds);
+                hipLaunchKernelGGL(kern, dim3((unsigned)pg), dim3(Cfg::NT), lds, st, a);
+                return;
+            }
+        }
         auto kern = lds_gemm_kernel<EPI, kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
         allow_dynamic_lds((const void*)kern, Cfg::LDS_BYTES);
         hipLaunchKernelGGL(kern, dim3((unsigned)blocks, (unsigned)batch), dim3(Cfg::NT), Cfg::LDS_BYTES, st, a);

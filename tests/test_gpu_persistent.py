@@ -1,0 +1,135 @@
+"""GPU parity of the persistent dequant / int32 GEMM (one continuous DMA stage stream per workgroup).
+
+The default launch goes persistent only when a problem has more tiles than the device has CUs, so
+these tests force a small grid with CANNBENCH_AMD_PERSISTENT_GRID: every workgroup then walks many
+tiles.  Together the cases cover an odd number of K stages (the ring rotates between tiles), K of
+exactly the ring's depth, K shorter than the ring (launched one tile per workgroup instead), ragged
+and empty groups, partial row and column tiles, every dequant flag, and the last tile's stages that
+fetch nothing.  The bar is the same as the non-persistent path: bit-exact against the oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def bits16(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def rand_i8(shape, g):
+    return torch.randint(-127, 128, shape, dtype=torch.int8, generator=g).to(DEV)
+
+
+def cpu_gen(seed):
+    g = torch.Generator()
+    g.manual_seed(seed)
+    return g
+
+
+@pytest.fixture(params=[3, 5])
+def small_grid(request, monkeypatch):
+    monkeypatch.setenv("CANNBENCH_AMD_PERSISTENT_GRID", str(request.param))
+    return request.param
+
+
+GMQ_CASES = [
+    # (counts, K, N): K stages of 128 -> 3 (odd), 4, 2 (the ring's depth), 1 (not persistent)
+    ([300, 0, 45, 600, 1, 0, 33], 384, 784),
+    ([270, 40], 400, 784),
+    ([520, 17, 0], 256, 512),
+    ([520, 17, 0], 96, 512),
+]
+
+
+@pytest.mark.parametrize("counts,K,N", GMQ_CASES)
+def test_persistent_grouped_matmul_quant(cb, orc, small_grid, counts, K, N):
+    g = cpu_gen(K + N + len(counts))
+    E, M = len(counts), sum(counts)
+    x = rand_i8((M, K), g)
+    w = rand_i8((E, K, N), g)
+    ws = (torch.rand(E, N, generator=g) * 0.009 + 0.001).to(DEV)
+    xs = (torch.rand(M, generator=g) * 0.015 + 0.005).to(DEV)
+    gl = np.cumsum(counts).tolist()
+    out = cb.grouped_matmul_quant(x, w, ws, xs, gl)
+    ref = orc.grouped_matmul_quant(x.cpu().numpy(), w.cpu().numpy(), ws.cpu().numpy(), xs.cpu().numpy(),
+                                   np.array(gl))
+    np.testing.assert_array_equal(bits16(out), ref)
+
+
+@pytest.mark.parametrize("counts,K,N", [([40, 0, 129, 7, 256], 1024, 768), ([300, 77], 384, 272)])
+def test_persistent_grouped_matmul_int32(cb, orc, small_grid, counts, K, N):
+    g = cpu_gen(K * 3 + N)
+    E = len(counts)
+    x = rand_i8((sum(counts), K), g)
+    w = rand_i8((E, K, N), g)
+    c = cb.grouped_matmul_int32(x, w, np.cumsum(counts).tolist()).cpu().numpy()
+    xn, wn = x.cpu().numpy(), w.cpu().numpy()
+    s = 0
+    for e, cnt in enumerate(counts):
+        if cnt:
+            np.testing.assert_array_equal(c[s:s + cnt], orc.i8_gemm(xn[s:s + cnt], wn[e]), err_msg=f"group {e}")
+        s += cnt
+
+
+@pytest.mark.parametrize("variant", ["pertoken_bf16", "offset_bias_f32", "bias_i32_scalar_scale",
+                                     "bf16_scale_f16_out", "default_fp16"])
+def test_persistent_quant_matmul_flags(cb, orc, small_grid, variant):
+    g = cpu_gen(91)
+    M, K, N = 600, 384, 528  # 3 x 3 tiles, the last column tile 16 wide
+    x1 = rand_i8((M, K), g)
+    x2 = rand_i8((K, N), g)
+    scale = torch.rand(N, generator=g) * 0.009 + 0.001
+    pt = torch.rand(M, generator=g) * 0.015 + 0.005
+    kw, okw = {"pertoken_scale": pt.to(DEV), "output_dtype": "bfloat16"}, {"pertoken": pt.numpy(), "out_dtype": "bf16"}
+    if variant == "offset_bias_f32":
+        off = torch.rand(N, generator=g) - 0.5
+        bias = torch.rand(N, generator=g) * 4 - 2
+        kw.update(offset=off.to(DEV), bias=bias.to(DEV))
+        okw.update(offset=off.numpy(), bias=bias.numpy(), bias_dtype="f32")
+    elif variant == "bias_i32_scalar_scale":
+        scale = scale[:1]
+        bias = torch.randint(-1000, 1000, (N,), dtype=torch.int32, generator=g)
+        kw.update(bias=bias.to(DEV))
+        okw.update(bias=bias.numpy(), bias_dtype="i32")
+    elif variant == "bf16_scale_f16_out":
+        scale = scale.to(torch.bfloat16)
+        kw["output_dtype"] = "float16"
+        okw.update(scale_dtype="bf16", out_dtype="f16")
+    elif variant == "default_fp16":
+        kw, okw = {}, {"out_dtype": "f16"}
+    out = cb.quant_matmul(x1, x2, scale.to(DEV), **kw)
+    sc_np = bits16(scale) if scale.dtype == torch.bfloat16 else scale.numpy()
+    ref = orc.quant_matmul(x1.cpu().numpy(), x2.cpu().numpy(), sc_np, **okw)
+    np.testing.assert_array_equal(bits16(out).reshape(ref.shape), ref)
+
+
+def test_persistent_default_grid_matches_one_tile_per_workgroup(cb, monkeypatch):
+    """More tiles than CUs: the default launch is persistent; bit-identical to the launch with one
+    tile per workgroup (persistent launch off) and to the oracle's int32 products on a sample."""
+    g = cpu_gen(5)
+    counts = [600, 13, 0, 700, 256, 640, 1, 550, 900]  # 19 row tiles x 16 column tiles > 256
+    K, N = 256, 4096
+    E, M = len(counts), sum(counts)
+    x = rand_i8((M, K), g)
+    w = rand_i8((E, K, N), g)
+    ws = (torch.rand(E, N, generator=g) * 0.009 + 0.001).to(DEV)
+    xs = (torch.rand(M, generator=g) * 0.015 + 0.005).to(DEV)
+    gl = np.cumsum(counts).tolist()
+    a = cb.grouped_matmul_quant(x, w, ws, xs, gl)
+    c = cb.grouped_matmul_int32(x, w, gl)
+    monkeypatch.setenv("CANNBENCH_AMD_PERSISTENT_GRID", "0")
+    b = cb.grouped_matmul_quant(x, w, ws, xs, gl)
+    d = cb.grouped_matmul_int32(x, w, gl)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.equal(c, d)
+    # int32 products of every group's first and last rows against a CPU int64 product
+    xn, wn, cn = x.cpu().numpy().astype(np.int64), w.cpu().numpy().astype(np.int64), c.cpu().numpy()
+    s = 0
+    for e, cnt in enumerate(counts):
+        for r in {s, s + cnt - 1} if cnt else ():
+            np.testing.assert_array_equal(cn[r], xn[r] @ wn[e], err_msg=f"group {e} row {r}")
+        s += cnt
