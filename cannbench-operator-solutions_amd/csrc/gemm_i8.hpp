@@ -215,6 +215,103 @@ __device__ __forceinline__ void set_comp(uint4& v, int i, u32 x)
     else v.w = x;
 }
 
+// One 64-deep chunk of a skinny tile: the lane's activation operand (first, so waiting for it never
+// waits for weights issued later) and 16 weight rows; rows past K (and rows outside the activation
+// resource) read as zeros.
+__device__ __forceinline__ void skinny_load_chunk(__amdgpu_buffer_rsrc_t xres, __amdgpu_buffer_rsrc_t wres,
+                                                  const uint32_t lane_off, const uint32_t n, const int q,
+                                                  const int kc, uint4 (&R)[16], v4i& A)
+{
+    A = __builtin_amdgcn_raw_buffer_load_b128(xres, (uint32_t)(kc * 64 + q * 16), 0, 0);
+    const uint32_t kofs = (uint32_t)(kc * 64) * n;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) R[i] = buf_load16(wres, lane_off + kofs + (uint32_t)i * n);
+}
+
+// The chunk's MFMAs: the 16 loaded rows are transposed in registers into 16 B operands, one per
+// column, and MFMA j accumulates column 16 c + j.
+__device__ __forceinline__ void skinny_mma_chunk(const uint4 (&R)[16], const v4i av, v4i (&acc)[16])
+{
+    // column block cb: the 4 B operands of columns 4 cb .. 4 cb + 3, built from dword cb of the 16
+    // loaded rows, consumed right away to keep the live range short
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+        uint4 T[4];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            u32 o0, o1, o2, o3;
+            transpose4x4_b8(comp(R[4 * rb + 0], cb), comp(R[4 * rb + 1], cb), comp(R[4 * rb + 2], cb),
+                            comp(R[4 * rb + 3], cb), o0, o1, o2, o3);
+            set_comp(T[0], rb, o0);
+            set_comp(T[1], rb, o1);
+            set_comp(T[2], rb, o2);
+            set_comp(T[3], rb, o3);
+        }
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4)
+            acc[4 * cb + s4] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, as_v4i(T[s4]), acc[4 * cb + s4], 0, 0, 0);
+    }
+}
+
+// Epilogue of one output row of a skinny tile: lane (q, c) holds s[j] = C[row][ocol + j] (SwiGLU:
+// gate columns in lanes c < 8, their up partners 8 lanes away).  Every lane of the wave calls it.
+template <int EPI>
+__device__ __forceinline__ void skinny_row_epilogue(const GemmArgs& a, const int g, const int64_t b, const int row,
+                                                    const bool rowok, const bool colok, const int64_t ocol,
+                                                    const int64_t col, const int c, const int (&s)[16])
+{
+    const int64_t N = a.N;
+    const EpiArgs& e = a.epi;
+    (void)col;
+    if constexpr (EPI == EPI_SWIGLU) {
+        const int64_t H = e.H;
+        int u[16];  // the up-projection partner column sits 8 lanes away
+#pragma unroll
+        for (int j = 0; j < 16; ++j) u[j] = __shfl_xor(s[j], 8, 64);
+        float m = 0.0f;
+        if (c < 8 && rowok && colok) {
+            const float xs = src_x_scale(a, row);
+            const float* wsg = e.w_scale + (int64_t)g * N + opaque(ocol);
+            const float* wsu = wsg + H;
+            float act[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                act[j] = swiglu((float)s[j], (float)u[j], xs, wsg[j], wsu[j]);
+                m = fmaxf(m, fabsf(act[j]));
+            }
+            float4* dst = reinterpret_cast<float4*>(e.act + (int64_t)row * H + ocol);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                dst[j] = make_float4(act[4 * j], act[4 * j + 1], act[4 * j + 2], act[4 * j + 3]);
+        }
+        m = fmaxf(m, __shfl_xor(m, 1, 64));
+        m = fmaxf(m, __shfl_xor(m, 2, 64));
+        m = fmaxf(m, __shfl_xor(m, 4, 64));
+        if (c == 0 && rowok) atomicMax(e.amax + row, __float_as_uint(m));
+    } else if constexpr (EPI == EPI_I32) {
+        if (rowok && colok) {
+            int4* dst = reinterpret_cast<int4*>((int32_t*)e.out + b * e.out_bstride + (int64_t)row * N + ocol);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dst[j] = make_int4(s[4 * j], s[4 * j + 1], s[4 * j + 2], s[4 * j + 3]);
+        }
+    } else {
+        if (rowok && colok) {
+            const float pt = e.has_pt ? e.pertoken[row] : 1.0f;
+            const int64_t oc = opaque(ocol);
+            u32 packed[8];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const float v = apply_deq(e, col_deq(e, g, b, oc + j), s[j], pt);
+                const u32 h = e.out_bf16 ? f32_to_bf16(v) : f32_to_f16(v);
+                packed[j / 2] = (j & 1) ? (packed[j / 2] | (h << 16)) : h;
+            }
+            uint4* dst = reinterpret_cast<uint4*>((uint16_t*)e.out + b * e.out_bstride + (int64_t)row * N + ocol);
+            dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+            dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+        }
+    }
+}
+
 // ============================================================================================
 // skinny_kernel: decode-shaped groups.
 //   grid = (ntiles, E), block = 256 (4 waves).  SwiGLU tiles cover 128 gate + 128 up columns,
@@ -290,33 +387,9 @@ __global__ __launch_bounds__(256, PREFETCH ? 2 : CB_SKINNY_OCC) void skinny_kern
         // one chunk = the activation operand (first, so waiting for it never waits for weights
         // issued later) and 16 weight rows
         auto load_chunk = [&](int kc, uint4 (&R)[16], v4i& A) {
-            A = __builtin_amdgcn_raw_buffer_load_b128(xres, (uint32_t)(kc * 64 + q * 16), 0, 0);
-            const uint32_t kofs = (uint32_t)(kc * 64) * (uint32_t)N;  // rows past K read as zeros
-#pragma unroll
-            for (int i = 0; i < 16; ++i) R[i] = buf_load16(wres, lane_off + kofs + (uint32_t)i * (uint32_t)N);
+            skinny_load_chunk(xres, wres, lane_off, (uint32_t)N, q, kc, R, A);
         };
-        auto mma_chunk = [&](const uint4 (&R)[16], const v4i av) {
-            // column block cb: the 4 B operands of columns 4 cb .. 4 cb + 3, built from dword cb
-            // of the 16 loaded rows, consumed right away to keep the live range short
-#pragma unroll
-            for (int cb = 0; cb < 4; ++cb) {
-                uint4 T[4];
-#pragma unroll
-                for (int rb = 0; rb < 4; ++rb) {
-                    u32 o0, o1, o2, o3;
-                    transpose4x4_b8(comp(R[4 * rb + 0], cb), comp(R[4 * rb + 1], cb),
-                                    comp(R[4 * rb + 2], cb), comp(R[4 * rb + 3], cb), o0, o1, o2, o3);
-                    set_comp(T[0], rb, o0);
-                    set_comp(T[1], rb, o1);
-                    set_comp(T[2], rb, o2);
-                    set_comp(T[3], rb, o3);
-                }
-#pragma unroll
-                for (int s4 = 0; s4 < 4; ++s4)
-                    acc[4 * cb + s4] =
-                        __builtin_amdgcn_mfma_i32_16x16x64_i8(av, as_v4i(T[s4]), acc[4 * cb + s4], 0, 0, 0);
-            }
-        };
+        auto mma_chunk = [&](const uint4 (&R)[16], const v4i av) { skinny_mma_chunk(R, av, acc); };
 
         if constexpr (PREFETCH) {
             // the next chunk of this wave is always issued (chunks past K read zeros and fetch
@@ -367,54 +440,7 @@ __global__ __launch_bounds__(256, PREFETCH ? 2 : CB_SKINNY_OCC) void skinny_kern
 
         // MFMA 16x16 C layout: lane l holds rows 4 (l / 16) + r, column l % 16.
         const int row = mb + 4 * q + wave;
-        const bool rowok = row < r1;
-        if constexpr (EPI == EPI_SWIGLU) {
-            const int64_t H = e.H;
-            int u[16];  // the up-projection partner column sits 8 lanes away
-#pragma unroll
-            for (int j = 0; j < 16; ++j) u[j] = __shfl_xor(s[j], 8, 64);
-            float m = 0.0f;
-            if (c < 8 && rowok && colok) {
-                const float xs = src_x_scale(a, row);
-                const float* wsg = e.w_scale + (int64_t)g * N + opaque(ocol);
-                const float* wsu = wsg + H;
-                float act[16];
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    act[j] = swiglu((float)s[j], (float)u[j], xs, wsg[j], wsu[j]);
-                    m = fmaxf(m, fabsf(act[j]));
-                }
-                float4* dst = reinterpret_cast<float4*>(e.act + (int64_t)row * H + ocol);
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    dst[j] = make_float4(act[4 * j], act[4 * j + 1], act[4 * j + 2], act[4 * j + 3]);
-            }
-            m = fmaxf(m, __shfl_xor(m, 1, 64));
-            m = fmaxf(m, __shfl_xor(m, 2, 64));
-            m = fmaxf(m, __shfl_xor(m, 4, 64));
-            if (c == 0 && rowok) atomicMax(e.amax + row, __float_as_uint(m));
-        } else if constexpr (EPI == EPI_I32) {
-            if (rowok && colok) {
-                int4* dst = reinterpret_cast<int4*>((int32_t*)e.out + b * e.out_bstride + (int64_t)row * N + ocol);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) dst[j] = make_int4(s[4 * j], s[4 * j + 1], s[4 * j + 2], s[4 * j + 3]);
-            }
-        } else {
-            if (rowok && colok) {
-                const float pt = e.has_pt ? e.pertoken[row] : 1.0f;
-                const int64_t oc = opaque(ocol);
-                u32 packed[8];
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const float v = apply_deq(e, col_deq(e, g, b, oc + j), s[j], pt);
-                    const u32 h = e.out_bf16 ? f32_to_bf16(v) : f32_to_f16(v);
-                    packed[j / 2] = (j & 1) ? (packed[j / 2] | (h << 16)) : h;
-                }
-                uint4* dst = reinterpret_cast<uint4*>((uint16_t*)e.out + b * e.out_bstride + (int64_t)row * N + ocol);
-                dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-                dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
-            }
-        }
+        skinny_row_epilogue<EPI>(a, g, b, row, row < r1, colok, ocol, col, c, s);
     }
 }
 
