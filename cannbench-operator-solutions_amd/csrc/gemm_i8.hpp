@@ -365,7 +365,7 @@ __global__ __launch_bounds__(256, PREFETCH ? 2 : CB_SKINNY_OCC) void skinny_kern
         col = ocol;
     }
     const int64_t b = blockIdx.z;  // batch (dense QuantMatmul)
-    // weight block of this group; the host guarantees K * N < 2^31
+    // weight block of this group (the host sends K * N >= 2^31 to the generic kernels)
     const __amdgpu_buffer_rsrc_t wres = make_rsrc(a.w + b * a.w_bstride + (int64_t)g * a.w_gstride, (uint32_t)(K * N));
     const uint32_t lane_off = (uint32_t)(colok ? col : 0) + (uint32_t)(q * 16) * (uint32_t)N;
     const int nch = (int)((K + 63) >> 6);

@@ -11,6 +11,11 @@ namespace cb {
 
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// The vector GEMM paths address one group's [K, N] weight block (and a tile's activation rows)
+// through buffer resources with 32-bit byte offsets; larger blocks take the generic kernels, which
+// index in 64 bits.
+inline bool offsets32_ok(int64_t K, int64_t N) { return K * N < (1LL << 31); }
+
 // Cumsum group boundaries plus the prefix of M-tiles per group, passed by value to the grouped
 // kernels (no host->device copy, no device allocation).  row_end[g] is the exclusive end row of
 // group g; tile_start[g] is the first M-tile of group g in the launch's tile enumeration.

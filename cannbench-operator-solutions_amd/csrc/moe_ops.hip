@@ -305,8 +305,8 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
     a.epi.yq = y;
     a.epi.yq_scale = y_scale;
 
-    const bool fast = K > 0 && K % 16 == 0 && H % 16 == 0 && aligned(x, 16) && aligned(weight, 16) &&
-                      aligned(act, 16) && aligned(weight_scale, 4);
+    const bool fast = K > 0 && K % 16 == 0 && H % 16 == 0 && offsets32_ok(K, N) && aligned(x, 16) &&
+                      aligned(weight, 16) && aligned(act, 16) && aligned(weight_scale, 4);
     if (fast && kUseLdsCore && kFusedRequant) {
         // persistent GEMM with the requant fused: every column tile of a row tile is resident at once
         build_group_table(a.gt, group_list, E, 256);
@@ -400,8 +400,8 @@ extern "C" int cb_grouped_matmul_quant(const int8_t* x, const int8_t* weight, co
     a.epi.has_pt = 1;
     a.epi.out = out;
     a.epi.out_bf16 = 1;
-    const bool fast = K > 0 && K % 16 == 0 && N % 16 == 0 && aligned(x, 16) && aligned(weight, 16) &&
-                      aligned(out, 16);
+    const bool fast = K > 0 && K % 16 == 0 && N % 16 == 0 && offsets32_ok(K, N) && aligned(x, 16) &&
+                      aligned(weight, 16) && aligned(out, 16);
     launch_gemm<EPI_DEQUANT>(a, group_list, E, 1, fast, (hipStream_t)stream);
     return check_launch();
 }
@@ -472,7 +472,8 @@ extern "C" int cb_quant_matmul(const int8_t* x1, const int8_t* x2, const void* s
     e.out_bf16 = out_dtype == CB_DT_BFLOAT16;
     e.out_bstride = M * N;
     const int64_t gl[1] = {M};
-    const bool fast = K % 16 == 0 && N % 16 == 0 && aligned(x1, 16) && aligned(x2, 16) && aligned(out, 16);
+    const bool fast = K % 16 == 0 && N % 16 == 0 && offsets32_ok(K, N) && aligned(x1, 16) && aligned(x2, 16) &&
+                      aligned(out, 16);
     launch_gemm<EPI_DEQUANT>(a, gl, 1, batch, fast, (hipStream_t)stream);
     return check_launch();
 }
@@ -497,8 +498,8 @@ extern "C" int cb_grouped_matmul_int32(const int8_t* x, const int8_t* weight, co
     a.N = N;
     a.w_gstride = K * N;
     a.epi.out = c;
-    const bool fast = K > 0 && K % 16 == 0 && N % 16 == 0 && aligned(x, 16) && aligned(weight, 16) &&
-                      aligned(c, 16);
+    const bool fast = K > 0 && K % 16 == 0 && N % 16 == 0 && offsets32_ok(K, N) && aligned(x, 16) &&
+                      aligned(weight, 16) && aligned(c, 16);
     launch_gemm<EPI_I32>(a, group_list, E, 1, fast, (hipStream_t)stream);
     return check_launch();
 }

@@ -279,6 +279,24 @@ def test_quant_matmul_flags(cb, orc, variant):
     np.testing.assert_array_equal(bits16(out).reshape(ref.shape), ref)
 
 
+def test_weight_block_past_32bit_offsets(cb):
+    """A 4 GiB weight block (K * N = 2^32) is past the 32-bit buffer offsets of the vector paths and
+    must take the 64-bit generic kernel: sampled columns bit-exact against an int64 product."""
+    M, K, N = 2, 65536, 65536
+    g = torch.Generator(device=DEV)
+    g.manual_seed(7)
+    x1 = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=DEV, generator=g)
+    x2 = torch.randint(-127, 128, (K, N), dtype=torch.int8, device=DEV, generator=g)
+    sc = torch.rand(N, device=DEV, generator=g) * 0.009 + 0.001
+    pt = torch.rand(M, device=DEV, generator=g) * 0.015 + 0.005
+    out = cb.quant_matmul(x1, x2, sc, pertoken_scale=pt, output_dtype="bfloat16")
+    cols = torch.tensor([0, 1, 255, 4096, 30000, 32767, 32768, 50001, N - 17, N - 2, N - 1], device=DEV)
+    c = (x1.long()[:, :, None] * x2[:, cols].long()[None]).sum(1)  # exact int64 [M, len(cols)]
+    ref = ((c.float() * sc[cols]) * pt[:, None]).to(torch.bfloat16)
+    del x2
+    assert torch.equal(out[:, cols].view(torch.int16), ref.view(torch.int16))
+
+
 # ---------------------------------------------------------------------------------------------
 # int8 grouped down-projection
 # ---------------------------------------------------------------------------------------------
