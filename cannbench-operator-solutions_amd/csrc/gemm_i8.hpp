@@ -739,63 +739,74 @@ __device__ __forceinline__ int group_of_row(const GroupTable& gt, int row)
     return lo;
 }
 
+// The generic kernels walk virtual blocks vb = (row, 256-column tile) with a grid-stride loop, so
+// any M x tiles count fits a launch (a dispatch counts its work-items in 32 bits).
 __global__ __launch_bounds__(256) void generic_swiglu_kernel(const GemmArgs a)
 {
     const int64_t H = a.epi.H;
-    const int row = (int)(blockIdx.x / a.ntiles);
-    const int64_t idx = (int64_t)(blockIdx.x % a.ntiles) * 256 + threadIdx.x;
-    const bool ok = idx < H;
-    const int g = group_of_row(a.gt, row);
-    float v = 0.0f;
-    if (ok) {
-        const int srow = src_row(a, row);
-        const int8_t* xr = a.x + (int64_t)(srow >= 0 ? srow : 0) * a.K;
-        const int8_t* wg = a.w + (int64_t)g * a.w_gstride;
-        int cg = 0, cu = 0;
-        for (int64_t k = 0; k < a.K; ++k) {
-            const int xv = srow >= 0 ? xr[k] : 0;
-            cg += xv * (int)wg[k * a.N + idx];
-            cu += xv * (int)wg[k * a.N + H + idx];
+    const int64_t nvb = a.M * a.ntiles;
+    for (int64_t vb = blockIdx.x; vb < nvb; vb += gridDim.x) {
+        const int row = (int)(vb / a.ntiles);
+        const int64_t idx = (vb % a.ntiles) * 256 + threadIdx.x;
+        const bool ok = idx < H;
+        const int g = group_of_row(a.gt, row);
+        float v = 0.0f;
+        if (ok) {
+            const int srow = src_row(a, row);
+            const int8_t* xr = a.x + (int64_t)(srow >= 0 ? srow : 0) * a.K;
+            const int8_t* wg = a.w + (int64_t)g * a.w_gstride;
+            int cg = 0, cu = 0;
+            for (int64_t k = 0; k < a.K; ++k) {
+                const int xv = srow >= 0 ? xr[k] : 0;
+                cg += xv * (int)wg[k * a.N + idx];
+                cu += xv * (int)wg[k * a.N + H + idx];
+            }
+            v = swiglu((float)cg, (float)cu, src_x_scale(a, row), a.epi.w_scale[(int64_t)g * a.N + idx],
+                       a.epi.w_scale[(int64_t)g * a.N + H + idx]);
+            a.epi.act[(int64_t)row * H + idx] = v;
         }
-        v = swiglu((float)cg, (float)cu, src_x_scale(a, row), a.epi.w_scale[(int64_t)g * a.N + idx],
-                   a.epi.w_scale[(int64_t)g * a.N + H + idx]);
-        a.epi.act[(int64_t)row * H + idx] = v;
+        const float m = wave_max(ok ? fabsf(v) : 0.0f);
+        if ((threadIdx.x & 63) == 0) atomicMax(a.epi.amax + row, __float_as_uint(m));
     }
-    float m = wave_max(ok ? fabsf(v) : 0.0f);
-    if ((threadIdx.x & 63) == 0) atomicMax(a.epi.amax + row, __float_as_uint(m));
 }
 
 __global__ __launch_bounds__(256) void generic_dequant_kernel(const GemmArgs a)
 {
-    const int row = (int)(blockIdx.x / a.ntiles);
-    const int64_t col = (int64_t)(blockIdx.x % a.ntiles) * 256 + threadIdx.x;
     const int64_t b = blockIdx.y;
-    if (col >= a.N) return;
-    const int g = group_of_row(a.gt, row);
-    const int8_t* xr = a.x + b * a.x_bstride + (int64_t)row * a.K;
-    const int8_t* wg = a.w + b * a.w_bstride + (int64_t)g * a.w_gstride;
-    int acc = 0;
-    for (int64_t k = 0; k < a.K; ++k) acc += (int)xr[k] * (int)wg[k * a.N + col];
+    const int64_t nvb = a.M * a.ntiles;
     const EpiArgs& e = a.epi;
-    const ColDeq d = col_deq(e, g, b, col);
-    const float pt = e.has_pt ? e.pertoken[row] : 1.0f;
-    const float v = apply_deq(e, d, acc, pt);
-    uint16_t* ob = (uint16_t*)e.out + b * e.out_bstride;
-    ob[(int64_t)row * a.N + col] = e.out_bf16 ? f32_to_bf16(v) : f32_to_f16(v);
+    for (int64_t vb = blockIdx.x; vb < nvb; vb += gridDim.x) {
+        const int row = (int)(vb / a.ntiles);
+        const int64_t col = (vb % a.ntiles) * 256 + threadIdx.x;
+        if (col >= a.N) continue;
+        const int g = group_of_row(a.gt, row);
+        const int8_t* xr = a.x + b * a.x_bstride + (int64_t)row * a.K;
+        const int8_t* wg = a.w + b * a.w_bstride + (int64_t)g * a.w_gstride;
+        int acc = 0;
+        for (int64_t k = 0; k < a.K; ++k) acc += (int)xr[k] * (int)wg[k * a.N + col];
+        const ColDeq d = col_deq(e, g, b, col);
+        const float pt = e.has_pt ? e.pertoken[row] : 1.0f;
+        const float v = apply_deq(e, d, acc, pt);
+        uint16_t* ob = (uint16_t*)e.out + b * e.out_bstride;
+        ob[(int64_t)row * a.N + col] = e.out_bf16 ? f32_to_bf16(v) : f32_to_f16(v);
+    }
 }
 
 __global__ __launch_bounds__(256) void generic_i32_kernel(const GemmArgs a)
 {
-    const int row = (int)(blockIdx.x / a.ntiles);
-    const int64_t col = (int64_t)(blockIdx.x % a.ntiles) * 256 + threadIdx.x;
     const int64_t b = blockIdx.y;
-    if (col >= a.N) return;
-    const int g = group_of_row(a.gt, row);
-    const int8_t* xr = a.x + b * a.x_bstride + (int64_t)row * a.K;
-    const int8_t* wg = a.w + b * a.w_bstride + (int64_t)g * a.w_gstride;
-    int acc = 0;
-    for (int64_t k = 0; k < a.K; ++k) acc += (int)xr[k] * (int)wg[k * a.N + col];
-    ((int32_t*)a.epi.out + b * a.epi.out_bstride)[(int64_t)row * a.N + col] = acc;
+    const int64_t nvb = a.M * a.ntiles;
+    for (int64_t vb = blockIdx.x; vb < nvb; vb += gridDim.x) {
+        const int row = (int)(vb / a.ntiles);
+        const int64_t col = (vb % a.ntiles) * 256 + threadIdx.x;
+        if (col >= a.N) continue;
+        const int g = group_of_row(a.gt, row);
+        const int8_t* xr = a.x + b * a.x_bstride + (int64_t)row * a.K;
+        const int8_t* wg = a.w + b * a.w_bstride + (int64_t)g * a.w_gstride;
+        int acc = 0;
+        for (int64_t k = 0; k < a.K; ++k) acc += (int)xr[k] * (int)wg[k * a.N + col];
+        ((int32_t*)a.epi.out + b * a.epi.out_bstride)[(int64_t)row * a.N + col] = acc;
+    }
 }
 
 }  // namespace cb

@@ -16,6 +16,11 @@ inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintp
 // index in 64 bits.
 inline bool offsets32_ok(int64_t K, int64_t N) { return K * N < (1LL << 31); }
 
+// A dispatch counts its work-items (blocks x threads per dimension) in 32 bits.  The row kernels
+// launch one block per row (or per few rows); an operator whose launch would not fit returns
+// CB_ERR_SHAPE instead of launching a truncated grid.
+inline bool grid_fits(int64_t blocks, int64_t threads) { return blocks * threads < (1LL << 32); }
+
 // Cumsum group boundaries plus the prefix of M-tiles per group, passed by value to the grouped
 // kernels (no host->device copy, no device allocation).  row_end[g] is the exclusive end row of
 // group g; tile_start[g] is the first M-tile of group g in the launch's tile enumeration.

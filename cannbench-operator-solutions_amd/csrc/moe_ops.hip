@@ -18,11 +18,10 @@ namespace cb {
 // abs-max accumulated by the GEMM epilogue (gmsq_vec_kernel.cpp:233-257):
 //   amax <- FLT_MIN unless amax > FLT_MIN;  y_scale = amax * (1/127)
 //   y = rint16(clamp(act * (127 / amax), -128, 127))   (rint16 saturates)
-__global__ __launch_bounds__(256) void gmsq_requant_kernel(const float* __restrict__ act,
-                                                           const u32* __restrict__ amax, int64_t H,
-                                                           int8_t* __restrict__ y, float* __restrict__ ys)
+__device__ __forceinline__ void gmsq_requant_row(const float* __restrict__ act, const u32* __restrict__ amax,
+                                                 const int64_t row, const int64_t H, int8_t* __restrict__ y,
+                                                 float* __restrict__ ys)
 {
-    const int64_t row = blockIdx.x;
     float a = __uint_as_float(amax[row]);
     if (!(a > kFltMin)) a = kFltMin;
     if (threadIdx.x == 0) ys[row] = a * kInv127;
@@ -40,6 +39,14 @@ __global__ __launch_bounds__(256) void gmsq_requant_kernel(const float* __restri
     } else {
         for (int64_t j = threadIdx.x; j < H; j += 256) dst[j] = (int8_t)q(src[j]);
     }
+}
+
+// Rows blockIdx.x + i * gridDim.x: the grid is capped, since a dispatch counts its work-items in 32 bits.
+__global__ __launch_bounds__(256) void gmsq_requant_kernel(const float* __restrict__ act,
+                                                           const u32* __restrict__ amax, int64_t M, int64_t H,
+                                                           int8_t* __restrict__ y, float* __restrict__ ys)
+{
+    for (int64_t row = blockIdx.x; row < M; row += gridDim.x) gmsq_requant_row(act, amax, row, H, y, ys);
 }
 
 __global__ void fill_u32_kernel(u32* p, int64_t n, u32 v)
@@ -157,7 +164,8 @@ static void launch_gemm(GemmArgs& a, const int64_t* gl, int64_t E, int64_t batch
     build_group_table(a.gt, gl, E, kTiledBM);
     if (!fast) {
         a.ntiles = (int)((Ncols + 255) / 256);
-        const dim3 grid((unsigned)(a.M * a.ntiles), (unsigned)batch);
+        const int64_t vblocks = a.M * a.ntiles;  // the kernels loop over virtual blocks past the grid
+        const dim3 grid((unsigned)(vblocks < (1 << 20) ? vblocks : (1 << 20)), (unsigned)batch);
         if constexpr (EPI == EPI_SWIGLU)
             hipLaunchKernelGGL(generic_swiglu_kernel, grid, dim3(256), 0, st, a);
         else if constexpr (EPI == EPI_I32)
@@ -328,7 +336,8 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
     // row maxima and the status word start at zero on this path too
     fill_u32(amax, (ws.status_off - ws.amax_off) / 4 + 2, 0u, st);
     launch_gemm<EPI_SWIGLU>(a, group_list, E, 1, fast, st);
-    hipLaunchKernelGGL(gmsq_requant_kernel, dim3((unsigned)M), dim3(256), 0, st, act, amax, H, y, y_scale);
+    hipLaunchKernelGGL(gmsq_requant_kernel, dim3((unsigned)(M < 65536 ? M : 65536)), dim3(256), 0, st, act, amax, M,
+                       H, y, y_scale);
     return check_launch();
 }
 

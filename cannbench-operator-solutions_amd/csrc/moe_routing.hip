@@ -821,6 +821,7 @@ extern "C" int cb_moe_re_routing(const void* tokens, int tokens_dtype, int64_t A
     const RerouteWs w = reroute_ws(n_ranks, n_experts);
     if (!workspace || workspace_bytes < w.total) return CB_ERR_WORKSPACE;
     hipStream_t st = (hipStream_t)stream;
+    if (!grid_fits((A + 3) / 4, 256)) return CB_ERR_SHAPE;  // the copy kernel: 4 rows per block
     TimedLaunch timed(st);
     uint8_t* wsb = (uint8_t*)workspace;
     int32_t* src = (int32_t*)(wsb + w.src_off);
@@ -891,6 +892,7 @@ extern "C" int cb_moe_finalize_routing(const void* expanded_permuted_rows, int d
                      (!skip1 || aligned(skip1, 16)) && (!skip2 || aligned(skip2, 16)) && (!a.bias || aligned(a.bias, 16));
     const dim3 grid((unsigned)num_rows);
     const dim3 block(vec ? row_threads(H / V) : 256);
+    if (!grid_fits(num_rows, block.x)) return CB_ERR_SHAPE;
 #define CB_MFR(DTV, SDTV)                                                                          \
     do {                                                                                           \
         if (vec) hipLaunchKernelGGL((mfr_vec_kernel<DTV, SDTV>), grid, block, 0, st, a);           \
@@ -972,6 +974,7 @@ extern "C" int cb_dequant_swiglu_quant(const void* x, int x_dtype, int64_t M, in
     threads = (threads + 63) / 64 * 64;
     threads = threads < 64 ? 64 : (threads > 512 ? 512 : threads);
     if (!reg) threads = 512;
+    if (!grid_fits(M, threads)) return CB_ERR_SHAPE;
     const dim3 block(threads);
 #define CB_DQSQ(XDTV)                                                                              \
     do {                                                                                           \
@@ -1004,6 +1007,7 @@ extern "C" int cb_moe_gating_top_k_softmax(const void* x, int dtype, int64_t row
     // E <= 256: 16 lanes per row (4 rows per wave); larger E: a whole wave per row
     const int lpr = E <= 256 ? 16 : 64;
     const int64_t rows_per_block = 4 * (64 / lpr);
+    if (!grid_fits((rows + rows_per_block - 1) / rows_per_block, 256)) return CB_ERR_SHAPE;
     const dim3 grid((unsigned)((rows + rows_per_block - 1) / rows_per_block)), block(256);
     int epl = (int)((E + lpr - 1) / lpr);
     epl = epl <= 1 ? 1 : epl <= 2 ? 2 : epl <= 4 ? 4 : epl <= 8 ? 8 : epl <= 16 ? 16 : 32;

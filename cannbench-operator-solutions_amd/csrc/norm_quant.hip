@@ -422,6 +422,7 @@ extern "C" int cb_add_rms_norm_dynamic_quant(const void* x1, const void* x2, con
     const bool al = aligned(x1, 16) && aligned(x2, 16) && aligned(gamma, 16) && aligned(x_out, 16) &&
                     aligned(y, 8);
     RowPlan p = plan_row(row_len, al);
+    if (!grid_fits(rows, p.threads)) return CB_ERR_SHAPE;
     const float invN = 1.0f / (float)row_len;
     hipStream_t st = (hipStream_t)stream;
     TimedLaunch timed(st);
@@ -448,6 +449,7 @@ extern "C" int cb_dynamic_quant(const void* x, int dtype, int64_t rows, int64_t 
     if (rows == 0) return CB_OK;
     if (rows > 0x7fffffffLL) return CB_ERR_SHAPE;
     if (!x || !y || !scale) return CB_ERR_NULL_POINTER;
+    if (!grid_fits(rows, 512)) return CB_ERR_SHAPE;  // the widest block any path below uses
     hipStream_t st = (hipStream_t)stream;
     TimedLaunch timed(st);
     if (row_len > 16384) {  // longer than a register-resident row slice

@@ -155,6 +155,20 @@ def test_routing_validation(lib):
     assert so.cb_moe_gating_top_k_softmax(FAKE, 3, 0, 8, None, 2, FAKE, FAKE, FAKE, None) == L.CB_ERR_EMPTY
 
 
+def test_launch_grid_limits(lib):
+    """Row counts whose one-block-per-row launch would exceed the dispatch's 32-bit work-item count
+    are rejected before any device call; the same operators accept them below the limit (checked on
+    the GPU by the parity suites)."""
+    L, so = lib
+    big = (1 << 31) - 1
+    assert so.cb_dynamic_quant(FAKE, 1, 1 << 23, 64, FAKE, FAKE, None) == L.CB_ERR_SHAPE
+    assert so.cb_add_rms_norm_dynamic_quant(FAKE, FAKE, FAKE, 2, big, 64, 1e-6, FAKE, FAKE, FAKE, None) \
+        == L.CB_ERR_SHAPE
+    # H = 6 is off the vector path (whose persistent grid is bounded): one block per row
+    assert so.cb_dequant_swiglu_quant(FAKE, 1, big, 12, None, None, None, 0, FAKE, FAKE, None) == L.CB_ERR_SHAPE
+    assert so.cb_moe_gating_top_k_softmax(FAKE, 3, big, 8, None, 2, FAKE, FAKE, FAKE, None) == L.CB_ERR_SHAPE
+
+
 def test_gmsq_status_query_host_paths(lib):
     """The status query rejects NULL arguments and reports 0 for empty shapes, both before any
     device access."""

@@ -166,6 +166,31 @@ def test_gmsq(cb, orc, counts, K, N):
     assert_int8_close(np_i8(y), yr, label="gmsq y")
 
 
+def test_generic_paths_past_their_grid(cb, orc):
+    """The generic kernels and the requant kernel cap their grids and loop over the rest: more
+    virtual blocks (rows x 256-column tiles) than the 2^20-block grid, and more rows than the
+    requant kernel's 65536 blocks (K = 8 is off the vector paths)."""
+    g = cpu_gen(2024)
+    counts = [(1 << 19) + 700, 0, 77]  # x 2 column tiles: 1050130 virtual blocks
+    E, M, K, N = len(counts), sum(counts), 8, 272
+    x = rand_i8((M, K), g)
+    w = rand_i8((E, K, N), g)
+    gl = np.cumsum(counts).tolist()
+    c = cb.grouped_matmul_int32(x, w, gl).cpu().numpy()
+    xn, wn = np_i8(x).astype(np.int64), np_i8(w).astype(np.int64)
+    s0 = 0
+    for e, cnt in enumerate(counts):
+        if cnt:
+            np.testing.assert_array_equal(c[s0:s0 + cnt], xn[s0:s0 + cnt] @ wn[e], err_msg=f"group {e}")
+        s0 += cnt
+    del c
+    x2, w2, ws2, xs2, gl2 = _gmsq_inputs([40000, 30001], 8, 64, 99)
+    y, ys = cb.grouped_matmul_swiglu_quant(x2, w2, ws2, xs2, gl2)
+    yr, ysr = orc.gmsq(np_i8(x2), np_i8(w2), ws2.cpu().numpy(), xs2.cpu().numpy(), np.array(gl2))
+    np.testing.assert_allclose(ys.cpu().numpy(), ysr, rtol=1e-5)
+    assert_int8_close(np_i8(y), yr, label="gmsq y")
+
+
 @pytest.mark.parametrize("seed", [0, 1, 2])
 def test_gmsq_fused_random_routing(cb, orc, seed):
     """The persistent fused-requant GEMM with its 256-workgroup slot mapping (N = 4096: 16 column
