@@ -82,7 +82,9 @@ struct LdsCfg {
     // [256][128]) with a 16-byte row pad that keeps rows 4 apart off the same banks
     static constexpr int EPI_PITCH = 528;
     static constexpr int EPI_BYTES = BM * EPI_PITCH;
-    static constexpr int LDS_BYTES = STAGES * STAGE > EPI_BYTES ? STAGES * STAGE : EPI_BYTES;
+    // the tile's per-row activation scales (SwiGLU epilogues), after the ring / staging area
+    static constexpr int XS_OFF = STAGES * STAGE > EPI_BYTES ? STAGES * STAGE : EPI_BYTES;
+    static constexpr int LDS_BYTES = XS_OFF + BM * 4;
     static constexpr int A_ISSUE = A_BYTES / 16 / NT;  // DMA instructions per thread per stage
     static constexpr int B_ISSUE = B_BYTES / 16 / NT;
     static constexpr int ISSUE = A_ISSUE + B_ISSUE;
@@ -299,6 +301,14 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
     if constexpr (!CONT) {
 #pragma unroll
         for (int st = 0; st < STAGES; ++st) issue_stage(st);
+    }
+    // SwiGLU epilogues: each thread fetches the activation scale of tile row tid % BM now (through
+    // the row index when gathered), so the load hides under the K loop; the epilogue hands the
+    // scales over through LDS.  Every thread loads (no divergent branch around the load).
+    float xs_pre = 0.0f;
+    if constexpr (SW) {
+        const int xr = m0 + tid % BM;
+        xs_pre = src_x_scale(a, xr < r1 ? xr : r1 - 1);
     }
 
     // Software pipeline per stage kt (fragments of half-stage ks = 0 already in registers):
@@ -543,6 +553,8 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
             wsg[fn] = ok ? e.w_scale[(int64_t)g * N + jc] : 0.0f;
             wsu[fn] = ok ? e.w_scale[(int64_t)g * N + H + jc] : 0.0f;
         }
+        CB_LDS float* xs_lds = (CB_LDS float*)((CB_LDS uint8_t*)smem + C::XS_OFF);
+        if (tid < BM) xs_lds[tid] = xs_pre;  // published by the barrier below
         epi_barrier();
         CB_LDS uint8_t* st = (CB_LDS uint8_t*)smem;
 #pragma unroll
@@ -551,8 +563,7 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int lrow = (WM * fm + wm) * 32 + (r >> 2) * 8 + lr + (r & 3);
-                const int row = m0 + lrow < r1 ? m0 + lrow : r1 - 1;
-                const float xs = src_x_scale(a, row);
+                const float xs = xs_lds[lrow];  // row min(m0 + lrow, r1 - 1)'s scale
 #pragma unroll
                 for (int fn = 0; fn < FN / 2; ++fn) {
                     const float v = swiglu((float)acc[fm][fn][r], (float)acc[fm][fn + FN / 2][r], xs, wsg[fn], wsu[fn]);
