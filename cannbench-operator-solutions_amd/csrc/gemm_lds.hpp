@@ -85,6 +85,9 @@ struct LdsCfg {
     // the tile's per-row activation scales (SwiGLU epilogues), after the ring / staging area
     static constexpr int XS_OFF = STAGES * STAGE > EPI_BYTES ? STAGES * STAGE : EPI_BYTES;
     static constexpr int LDS_BYTES = XS_OFF + BM * 4;
+    // persistent dequant / int32 kernel: the ring, then two row-scale slots (alternate tiles)
+    static constexpr int CONT_XS_OFF = STAGES * STAGE;
+    static constexpr int CONT_LDS_BYTES = CONT_XS_OFF + 2 * BM * 4;
     static constexpr int A_ISSUE = A_BYTES / 16 / NT;  // DMA instructions per thread per stage
     static constexpr int B_ISSUE = B_BYTES / 16 / NT;
     static constexpr int ISSUE = A_ISSUE + B_ISSUE;
@@ -208,7 +211,7 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
                                               uint8_t* smem, const int arr_idx = 0, const u32 arr_target = 0,
                                               const TileDmaOf<EPI, WM, WN, STAGES, BKT>* cur = nullptr,
                                               const TileDmaOf<EPI, WM, WN, STAGES, BKT>* nxt = nullptr,
-                                              const int sbase = 0)
+                                              const int sbase = 0, const int xs_slot = 0)
 {
     using C = LdsCfg<WM, WN, STAGES, BKT>;
     constexpr bool SW = EPI == EPI_SWIGLU || EPI == EPI_SWIGLU_Q;
@@ -302,13 +305,27 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
 #pragma unroll
         for (int st = 0; st < STAGES; ++st) issue_stage(st);
     }
-    // SwiGLU epilogues: each thread fetches the activation scale of tile row tid % BM now (through
-    // the row index when gathered), so the load hides under the K loop; the epilogue hands the
-    // scales over through LDS.  Every thread loads (no divergent branch around the load).
-    float xs_pre = 0.0f;
+    // Row scales of the epilogue (SwiGLU: the activation scale, through the row index when
+    // gathered; dequant: the per-token scale, 1 without one): each thread fetches the one of tile
+    // row tid % BM now, so the load hides under the K loop, and the epilogue reads them from LDS.
+    // Every thread loads (no branch around the load: an absent per-token scale reads through an
+    // empty resource).
+    float xs_pre = 1.0f;
     if constexpr (SW) {
         const int xr = m0 + tid % BM;
         xs_pre = src_x_scale(a, xr < r1 ? xr : r1 - 1);
+    } else if constexpr (EPI == EPI_DEQUANT) {
+        const int lr0 = tid % BM;
+        const __amdgpu_buffer_rsrc_t pres = e.has_pt ? make_rsrc(e.pertoken + m0, (uint32_t)(vrows * 4)) : make_rsrc(a.x, 0u);
+        const float v = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(pres, (uint32_t)((lr0 < vrows ? lr0 : vrows - 1) * 4), 0, 0));
+        xs_pre = e.has_pt ? v : 1.0f;
+    }
+    CB_LDS float* xs_lds = (CB_LDS float*)((CB_LDS uint8_t*)smem + (CONT ? C::CONT_XS_OFF + xs_slot * BM * 4 : C::XS_OFF));
+    if constexpr (CONT && EPI == EPI_DEQUANT) {
+        // no barrier of its own in this epilogue: the K loop's barriers publish the slot (the
+        // previous tile read the other one)
+        if (tid < BM) xs_lds[tid] = xs_pre;
     }
 
     // Software pipeline per stage kt (fragments of half-stage ks = 0 already in registers):
@@ -489,23 +506,13 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
                 cd[fn] = col_deq(e, g, b, cc < N ? cc : 0);
                 coff[fn] = cc < N ? (uint32_t)(cc & ~(int64_t)1) * 2u : 0x80000000u;
             }
-            // Every row scale is loaded before the first store: a load between stores would make
-            // its wait (vmcnt counts stores too) drain the stores issued before it.
+            // the row scales come from LDS (fetched under the K loop): no global load between the
+            // stores, whose wait would drain every store issued before it (vmcnt counts stores too)
             float ptv[FM][16];
-            if (e.has_pt) {
 #pragma unroll
-                for (int fm = 0; fm < FM; ++fm)
+            for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int lrow = (WM * fm + wm) * 32 + (r >> 2) * 8 + lr + (r & 3);
-                        ptv[fm][r] = e.pertoken[m0 + lrow < r1 ? m0 + lrow : r1 - 1];
-                    }
-            } else {
-#pragma unroll
-                for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) ptv[fm][r] = 1.0f;
-            }
+                for (int r = 0; r < 16; ++r) ptv[fm][r] = xs_lds[(WM * fm + wm) * 32 + (r >> 2) * 8 + lr + (r & 3)];
             auto store = [&](auto simple_const) {
                 constexpr bool SIMPLE = decltype(simple_const)::value;
 #pragma unroll
@@ -553,7 +560,6 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
             wsg[fn] = ok ? e.w_scale[(int64_t)g * N + jc] : 0.0f;
             wsu[fn] = ok ? e.w_scale[(int64_t)g * N + H + jc] : 0.0f;
         }
-        CB_LDS float* xs_lds = (CB_LDS float*)((CB_LDS uint8_t*)smem + C::XS_OFF);
         if (tid < BM) xs_lds[tid] = xs_pre;  // published by the barrier below
         epi_barrier();
         CB_LDS uint8_t* st = (CB_LDS uint8_t*)smem;
@@ -689,6 +695,7 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
             const int64_t cc = (int64_t)nt * BN + wn * TN + fn * 32 + (lane & 31);
             cd[fn] = col_deq(e, g, b, cc < N ? cc : 0);
         }
+        if (tid < BM) xs_lds[tid] = xs_pre;  // published by the barrier below
         epi_barrier();
         CB_LDS uint8_t* st = (CB_LDS uint8_t*)smem;
         // The flags are uniform: branch once per tile rather than per value, so the common chain
@@ -703,8 +710,7 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int lrow = (WM * fm + wm) * 32 + (r >> 2) * 8 + lr + (r & 3);
-                    const int row = m0 + lrow < r1 ? m0 + lrow : r1 - 1;
-                    const float pt = e.has_pt ? e.pertoken[row] : 1.0f;
+                    const float pt = xs_lds[lrow];  // 1 without a per-token scale
 #pragma unroll
                     for (int fn = 0; fn < FN; ++fn) {
                         uint16_t h;
@@ -795,7 +801,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_persistent_kernel(co
     cur.init(a, mt, nt, 0, wave, lane);
 #pragma unroll
     for (int st = 0; st < STAGES; ++st) cur.issue_at(st, st, lds_base, wave);
-    int sbase = 0;
+    int sbase = 0, xs_slot = 0;
     for (;;) {
         const int pn = pid + (int)gridDim.x;
         int mt2 = 0, nt2 = 0;
@@ -805,8 +811,9 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_persistent_kernel(co
         } else {
             nxt.set_dead(a);
         }
-        lds_gemm_tile<EPI, WM, WN, STAGES, BKT, true>(a, mt, nt, 0, smem, 0, 0, &cur, &nxt, sbase);
+        lds_gemm_tile<EPI, WM, WN, STAGES, BKT, true>(a, mt, nt, 0, smem, 0, 0, &cur, &nxt, sbase, xs_slot);
         if (pn >= total) break;
+        xs_slot ^= 1;
         sbase = (sbase + cur.nk) % STAGES;
         cur = nxt;
         pid = pn;

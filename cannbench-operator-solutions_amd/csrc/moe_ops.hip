@@ -206,7 +206,7 @@ static void launch_gemm(GemmArgs& a, const int64_t* gl, int64_t E, int64_t batch
             if (batch == 1 && pg > 0 && blocks > pg && a.K >= (int64_t)Cfg::STAGES_ * Cfg::BK &&
                 Cfg::BM * Ncols * 4 < 0x7fffffffLL) {
                 auto kern = lds_gemm_persistent_kernel<EPI, kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
-                constexpr int lds = Cfg::STAGES_ * Cfg::STAGE;  // the ring: the epilogue needs no LDS
+                constexpr int lds = Cfg::CONT_LDS_BYTES;  // the ring and two row-scale slots
                 allow_dynamic_lds((const void*)kern, lds);
                 hipLaunchKernelGGL(kern, dim3((unsigned)pg), dim3(Cfg::NT), lds, st, a);
                 return;
