@@ -83,11 +83,13 @@ struct LdsCfg {
     static constexpr int EPI_PITCH = 528;
     static constexpr int EPI_BYTES = BM * EPI_PITCH;
     // the tile's per-row activation scales (SwiGLU epilogues), after the ring / staging area
+    // and the column scales: one slot of BM + BN floats
     static constexpr int XS_OFF = STAGES * STAGE > EPI_BYTES ? STAGES * STAGE : EPI_BYTES;
-    static constexpr int LDS_BYTES = XS_OFF + BM * 4;
-    // persistent dequant / int32 kernel: the ring, then two row-scale slots (alternate tiles)
+    static constexpr int XS_SLOT = (BM + BN) * 4;
+    static constexpr int LDS_BYTES = XS_OFF + XS_SLOT;
+    // persistent dequant / int32 kernel: the ring, then two scale slots (alternate tiles)
     static constexpr int CONT_XS_OFF = STAGES * STAGE;
-    static constexpr int CONT_LDS_BYTES = CONT_XS_OFF + 2 * BM * 4;
+    static constexpr int CONT_LDS_BYTES = CONT_XS_OFF + 2 * XS_SLOT;
     static constexpr int A_ISSUE = A_BYTES / 16 / NT;  // DMA instructions per thread per stage
     static constexpr int B_ISSUE = B_BYTES / 16 / NT;
     static constexpr int ISSUE = A_ISSUE + B_ISSUE;
@@ -305,27 +307,50 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
 #pragma unroll
         for (int st = 0; st < STAGES; ++st) issue_stage(st);
     }
-    // Row scales of the epilogue (SwiGLU: the activation scale, through the row index when
-    // gathered; dequant: the per-token scale, 1 without one): each thread fetches the one of tile
-    // row tid % BM now, so the load hides under the K loop, and the epilogue reads them from LDS.
-    // Every thread loads (no branch around the load: an absent per-token scale reads through an
-    // empty resource).
-    float xs_pre = 1.0f;
+    // Scales of the epilogue, fetched now so the loads hide under the K loop; the epilogue reads
+    // them from LDS.  Row scales (SwiGLU: the activation scale, through the row index when
+    // gathered; dequant: the per-token scale, 1 without one): thread tid takes tile row tid % BM.
+    // Column scales (SwiGLU: w_scale of the 128 gate then the 128 up columns; dequant: the output
+    // scale): thread tid takes tile column tid % BN.  Every thread loads, with no branch around a
+    // load: absent operands read through empty buffer resources.
+    float xs_pre = 1.0f, cs_pre = 0.0f;
     if constexpr (SW) {
         const int xr = m0 + tid % BM;
         xs_pre = src_x_scale(a, xr < r1 ? xr : r1 - 1);
+        const int64_t H = e.H;
+        const int j = tid % BN;
+        const int64_t jc = (int64_t)nt * (BN / 2) + (j & (BN / 2 - 1));
+        const int64_t wc = j < BN / 2 ? jc : H + jc;
+        const __amdgpu_buffer_rsrc_t wsr = make_rsrc(e.w_scale + (int64_t)g * N, (uint32_t)(N * 4));
+        cs_pre = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                               wsr, jc < H ? (uint32_t)(wc * 4) : 0x80000000u, 0, 0));
     } else if constexpr (EPI == EPI_DEQUANT) {
         const int lr0 = tid % BM;
-        const __amdgpu_buffer_rsrc_t pres = e.has_pt ? make_rsrc(e.pertoken + m0, (uint32_t)(vrows * 4)) : make_rsrc(a.x, 0u);
+        const __amdgpu_buffer_rsrc_t pres =
+            e.has_pt ? make_rsrc(e.pertoken + m0, (uint32_t)(vrows * 4)) : make_rsrc(a.x, 0u);
         const float v = __builtin_bit_cast(
             float, __builtin_amdgcn_raw_buffer_load_b32(pres, (uint32_t)((lr0 < vrows ? lr0 : vrows - 1) * 4), 0, 0));
         xs_pre = e.has_pt ? v : 1.0f;
+        // output scale of column cc: fp32 or bf16, per channel or one per group / batch
+        const int64_t cc = (int64_t)nt * BN + tid % BN;
+        const int64_t si = (int64_t)g * e.scale_gstride + (e.scale_perchan ? (cc < N ? cc : 0) : 0);
+        const __amdgpu_buffer_rsrc_t s32 = make_rsrc(e.scale, e.scale_bf16 ? 0u : 0x80000000u);
+        const __amdgpu_buffer_rsrc_t s16 = make_rsrc(e.scale, e.scale_bf16 ? 0x80000000u : 0u);
+        const float f32 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(s32, (uint32_t)(si * 4), 0, 0));
+        const uint16_t b16 = __builtin_amdgcn_raw_buffer_load_b16(s16, (uint32_t)(si * 2), 0, 0);
+        cs_pre = e.scale_bf16 ? bf16_to_f32(b16) : f32;
     }
-    CB_LDS float* xs_lds = (CB_LDS float*)((CB_LDS uint8_t*)smem + (CONT ? C::CONT_XS_OFF + xs_slot * BM * 4 : C::XS_OFF));
+    CB_LDS float* xs_lds =
+        (CB_LDS float*)((CB_LDS uint8_t*)smem + (CONT ? C::CONT_XS_OFF + xs_slot * C::XS_SLOT : C::XS_OFF));
+    CB_LDS float* cs_lds = xs_lds + BM;
+    auto publish_scales = [&]() {
+        if (tid < BM) xs_lds[tid] = xs_pre;
+        if (tid < BN) cs_lds[tid] = cs_pre;
+    };
     if constexpr (CONT && EPI == EPI_DEQUANT) {
         // no barrier of its own in this epilogue: the K loop's barriers publish the slot (the
         // previous tile read the other one)
-        if (tid < BM) xs_lds[tid] = xs_pre;
+        publish_scales();
     }
 
     // Software pipeline per stage kt (fragments of half-stage ks = 0 already in registers):
@@ -500,10 +525,12 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
             const bool odd = lane & 1;
             ColDeq cd[FN];
             uint32_t coff[FN];
+            const bool full_chain = e.has_offset || e.bias_kind != BIAS_NONE;  // uniform
 #pragma unroll
             for (int fn = 0; fn < FN; ++fn) {
                 const int64_t cc = col0 + 32 * fn;
-                cd[fn] = col_deq(e, g, b, cc < N ? cc : 0);
+                if (full_chain) cd[fn] = col_deq(e, g, b, cc < N ? cc : 0);
+                else cd[fn] = ColDeq{cs_lds[wn * TN + fn * 32 + (lane & 31)], 0.0f, 0.0f};
                 coff[fn] = cc < N ? (uint32_t)(cc & ~(int64_t)1) * 2u : 0x80000000u;
             }
             // the row scales come from LDS (fetched under the K loop): no global load between the
@@ -552,16 +579,14 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
         // act tile [256 rows][128 act columns] fp32 staged in LDS, then written with 16-byte stores
         // and one row-max atomic per (row, tile)
         const int64_t H = e.H;
-        float wsg[FN / 2], wsu[FN / 2];
+        publish_scales();  // published by the barrier below
+        epi_barrier();
+        float wsg[FN / 2], wsu[FN / 2];  // 0 past H
 #pragma unroll
         for (int fn = 0; fn < FN / 2; ++fn) {
-            const int64_t jc = (int64_t)nt * (BN / 2) + wn * (TN / 2) + fn * 32 + (lane & 31);
-            const bool ok = jc < H;
-            wsg[fn] = ok ? e.w_scale[(int64_t)g * N + jc] : 0.0f;
-            wsu[fn] = ok ? e.w_scale[(int64_t)g * N + H + jc] : 0.0f;
+            wsg[fn] = cs_lds[wn * (TN / 2) + fn * 32 + (lane & 31)];
+            wsu[fn] = cs_lds[BN / 2 + wn * (TN / 2) + fn * 32 + (lane & 31)];
         }
-        if (tid < BM) xs_lds[tid] = xs_pre;  // published by the barrier below
-        epi_barrier();
         CB_LDS uint8_t* st = (CB_LDS uint8_t*)smem;
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm) {
@@ -689,14 +714,21 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
         }
     } else {
         // bf16 / fp16 tile [256][256] staged in LDS, then written with 16-byte stores
+        const bool full_chain = e.has_offset || e.bias_kind != BIAS_NONE;  // uniform
         ColDeq cd[FN];
+        if (full_chain) {
 #pragma unroll
-        for (int fn = 0; fn < FN; ++fn) {
-            const int64_t cc = (int64_t)nt * BN + wn * TN + fn * 32 + (lane & 31);
-            cd[fn] = col_deq(e, g, b, cc < N ? cc : 0);
+            for (int fn = 0; fn < FN; ++fn) {
+                const int64_t cc = (int64_t)nt * BN + wn * TN + fn * 32 + (lane & 31);
+                cd[fn] = col_deq(e, g, b, cc < N ? cc : 0);
+            }
         }
-        if (tid < BM) xs_lds[tid] = xs_pre;  // published by the barrier below
+        publish_scales();  // published by the barrier below
         epi_barrier();
+        if (!full_chain) {
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn) cd[fn] = ColDeq{cs_lds[wn * TN + fn * 32 + (lane & 31)], 0.0f, 0.0f};
+        }
         CB_LDS uint8_t* st = (CB_LDS uint8_t*)smem;
         // The flags are uniform: branch once per tile rather than per value, so the common chain
         // (per-channel scale, optional pertoken, no offset or bias, bf16 out: QuantMatmul and the
