@@ -30,6 +30,7 @@ L = importlib.import_module("cannbench-operator-solutions_amd._lib")
 METRIC = "GroupedMatmulSwigluQuant int8 TOPS (%MFMA peak) + decode HBM GB/s (%peak), 1 GPU"
 PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 MFMA, published
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, published
+PEAK_BF16_TFLOPS = 2500.0    # MI355X dense bf16 / fp16 MFMA, published
 
 
 class KernelTimer:
@@ -67,8 +68,9 @@ def time_op(fn, steps, warmup, timer=None):
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
-def roofline(bound, achieved, unit, traffic=None):
-    peak = PEAK_INT8_TOPS if bound == "mfma" else PEAK_HBM_GBS
+def roofline(bound, achieved, unit, traffic=None, peak=None):
+    if peak is None:
+        peak = PEAK_INT8_TOPS if bound == "mfma" else PEAK_HBM_GBS
     return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": traffic}
 
@@ -212,6 +214,28 @@ def bench_qmm(steps, warmup, dev):
     return {"ms": ms, "tops": ops / (ms * 1e-3) / 1e12, "gemm_kernel_ms": kms,
             "roofline": roofline("mfma", ops / (kms * 1e-3) / 1e12, "TFLOP/s"),
             "config": {"workload": "qmm", "M": M, "K": K, "N": N}}
+
+
+def bench_gmm(steps, warmup, dev):
+    """Context: GroupedMatmul, the reference's float grouped GEMM, in bf16 on 64 experts (its expert
+    limit) x 256 rows, K = N = 4096, with a bf16 bias; against the 2.5 PFLOP/s dense bf16 peak."""
+    E, rows, K, N = 64, 256, 4096, 4096
+    g = torch.Generator(device=dev)
+    g.manual_seed(31)
+    x = torch.randn(E * rows, K, device=dev, generator=g).to(torch.bfloat16)
+    w = torch.randn(E, K, N, device=dev, generator=g).to(torch.bfloat16)
+    b = torch.randn(E, N, device=dev, generator=g).to(torch.bfloat16)
+    gl = [rows * (i + 1) for i in range(E)]
+    flops = 2.0 * E * rows * K * N
+    fn = lambda: cb.grouped_matmul(x, w, gl, bias=b, split_item=2)
+    timer = KernelTimer(steps)
+    ms = time_op(fn, steps, warmup, timer)
+    kms = timer.mean_ms()
+    return {"value": round(flops / (ms * 1e-3) / 1e12, 1), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+            "kernel_ms": round(kms, 4),
+            "roofline": roofline("mfma", flops / (kms * 1e-3) / 1e12, "TFLOP/s", peak=PEAK_BF16_TFLOPS),
+            "config": {"workload": "grouped_matmul", "dtype": "bf16", "experts": E, "rows_per_expert": rows,
+                       "K": K, "N": N, "bias": "bf16", "transpose_weight": False}}
 
 
 def bench_vendor(steps, warmup, dev):
@@ -365,9 +389,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", default="prefill,gather,down_prefill,decode,ardq,qmm,routing,vendor",
+    ap.add_argument("--only", default="prefill,gather,down_prefill,decode,ardq,qmm,routing,gmm,vendor",
                     help="comma list of prefill, gather and down_prefill (need prefill), decode, ardq, qmm, "
-                         "routing, vendor, copy")
+                         "routing, gmm, vendor, copy")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -414,6 +438,8 @@ def main():
                       "roofline": q["roofline"], "config": q["config"]}
     if "routing" in only:
         out["routing"] = bench_routing(args.steps, args.warmup, dev)
+    if "gmm" in only:
+        out["grouped_matmul"] = bench_gmm(args.steps, args.warmup, dev)
     if "vendor" in only:
         out["vendor_int8_gemm"] = bench_vendor(args.steps, args.warmup, dev)
         out["mfma_probe"] = bench_mfma_probe(dev)

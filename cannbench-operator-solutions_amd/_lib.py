@@ -37,6 +37,7 @@ CB_DT_INT32 = 5
 CB_DT_INT64 = 6
 
 CB_MAX_EXPERTS = 256
+CB_GMM_MAX_EXPERTS = 64  # GroupedMatmul (GMM_MAX_E)
 CB_ARDQ_MAX_ROW = 16384
 
 _P = ctypes.c_void_p
@@ -59,6 +60,7 @@ SIGNATURES = {
     "cb_quant_matmul": (_I, [_P, _P, _P, _I, _I64, _P, _I64, _P, _I64, _P, _I, _I64, _I, _I64, _I64, _I64, _I64, _I, _P, _P]),
     "cb_grouped_matmul_quant": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P]),
     "cb_grouped_matmul_int32": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P]),
+    "cb_grouped_matmul": (_I, [_P, _P, _P, _I, _I, _P, _I64, _I64, _I64, _I64, _I64, _I, _P, _P]),
     "cb_moe_re_routing_workspace_size": (_I64, [_I64, _I64]),
     "cb_moe_re_routing": (_I, [_P, _I, _I64, _I64, _P, _I, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64, _P]),
     "cb_moe_finalize_routing": (_I, [_P, _I, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _I64, _P, _I, _P, _I, _P, _P]),

@@ -741,7 +741,7 @@ __device__ __forceinline__ int group_of_row(const GroupTable& gt, int row)
 
 // The generic kernels walk virtual blocks vb = (row, 256-column tile) with a grid-stride loop, so
 // any M x tiles count fits a launch (a dispatch counts its work-items in 32 bits).
-__global__ __launch_bounds__(256) void generic_swiglu_kernel(const GemmArgs a)
+static __global__ __launch_bounds__(256) void generic_swiglu_kernel(const GemmArgs a)
 {
     const int64_t H = a.epi.H;
     const int64_t nvb = a.M * a.ntiles;
@@ -770,7 +770,7 @@ __global__ __launch_bounds__(256) void generic_swiglu_kernel(const GemmArgs a)
     }
 }
 
-__global__ __launch_bounds__(256) void generic_dequant_kernel(const GemmArgs a)
+static __global__ __launch_bounds__(256) void generic_dequant_kernel(const GemmArgs a)
 {
     const int64_t b = blockIdx.y;
     const int64_t nvb = a.M * a.ntiles;
@@ -792,7 +792,7 @@ __global__ __launch_bounds__(256) void generic_dequant_kernel(const GemmArgs a)
     }
 }
 
-__global__ __launch_bounds__(256) void generic_i32_kernel(const GemmArgs a)
+static __global__ __launch_bounds__(256) void generic_i32_kernel(const GemmArgs a)
 {
     const int64_t b = blockIdx.y;
     const int64_t nvb = a.M * a.ntiles;

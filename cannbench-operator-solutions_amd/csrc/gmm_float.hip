@@ -1,0 +1,288 @@
+// gmm_float.hip - GroupedMatmul, the reference's float grouped GEMM (C ABI cb_grouped_matmul):
+//   y[rows_g] = x[rows_g] @ weight[g] (+ bias[g]),  rows_g = [group_list[g-1], group_list[g])
+// in the dtype of x (fp16, bf16 or fp32), weight [E, K, N] or, with transpose_weight, [E, N, K]
+// (operators/groupedmatmul/csrc/ops/grouped_matmul/op_plugin/grouped_matmul_plugin.cpp:14-17,
+// 116-183; op_kernel/grouped_matmul_kernel.cpp:15-17, 111-150).
+//
+// 16-bit inputs run on v_mfma_f32_32x32x16_{f16,bf16}: 128 x 128 output tiles (4 waves of 64 x 64),
+// 32-deep K stages double-buffered in LDS with both operands stored K-contiguous (the weight is
+// transposed on its way into LDS when it arrives N-contiguous), fp32 accumulation, the bias added
+// in fp32, one round-to-nearest-even narrowing.  fp32 inputs and shapes off the vector path
+// (K or N not a multiple of 8, misaligned operands, 32-bit offsets exceeded) take a plain fp32 loop.
+#include <cstring>
+
+#include "gemm_i8.hpp"
+
+namespace cb {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kGmmMaxExperts = 64;  // GMM_MAX_E (grouped_matmul_launch.h)
+constexpr int GF_BM = 128, GF_BN = 128, GF_BK = 32;
+constexpr int GF_PITCH = GF_BK + 8;  // elements per LDS row (80 B): a 16-lane b128 read phase hits 16 bank groups
+
+struct GmmFArgs {
+    const void* x;
+    const void* w;
+    const void* bias;
+    void* y;
+    int64_t M, K, N;
+    int32_t x_dt, bias_dt;  // cb_dtype codes; bias_dt 0 = no bias
+    int32_t trans, ntiles;
+    GroupTable gt;
+};
+
+__device__ __forceinline__ float gf_load(const void* p, int dt, int64_t i)
+{
+    if (dt == CB_DT_FLOAT32) return ((const float*)p)[i];
+    if (dt == CB_DT_BFLOAT16) return bf16_to_f32(((const uint16_t*)p)[i]);
+    return f16_to_f32(((const uint16_t*)p)[i]);
+}
+
+__device__ __forceinline__ void gf_store(void* p, int dt, int64_t i, float v)
+{
+    if (dt == CB_DT_FLOAT32) ((float*)p)[i] = v;
+    else if (dt == CB_DT_BFLOAT16) ((uint16_t*)p)[i] = f32_to_bf16_hw(v);
+    else ((uint16_t*)p)[i] = f32_to_f16(v);
+}
+
+// One 128 x 128 tile per workgroup: pid -> (row tile, column tile) with 4 row tiles per column sweep.
+template <bool BF16, bool TRANS>
+__global__ __launch_bounds__(256, 2) void gmm_mfma_kernel(const GmmFArgs a)
+{
+    __shared__ __attribute__((aligned(16))) uint16_t As[2][GF_BM * GF_PITCH];
+    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][GF_BN * GF_PITCH];  // [n][k]
+
+    constexpr int GROUP_M = 4;
+    const int pid = blockIdx.x;
+    const int T_m = a.gt.total_mtiles, T_n = a.ntiles;
+    const int per_group = GROUP_M * T_n;
+    const int first_m = (pid / per_group) * GROUP_M;
+    const int gsz = (T_m - first_m) < GROUP_M ? (T_m - first_m) : GROUP_M;
+    const int mt = first_m + (pid % per_group) % gsz;
+    const int nt = (pid % per_group) / gsz;
+
+    const int g = group_of_tile(a.gt, mt);
+    const int rs = g ? a.gt.row_end[g - 1] : 0;
+    const int r1 = a.gt.row_end[g];
+    const int m0 = rs + (mt - a.gt.tile_start[g]) * GF_BM;
+    const int vrows = r1 - m0;
+    const int n0 = nt * GF_BN;
+    const int64_t K = a.K, N = a.N;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // Operand streams through buffer resources (offsets outside a resource read zeros).
+    // A: rows [m0, r1) of x; thread chunks c = tid + 256 i: row c / 4, k chunk c % 4 (8 elements).
+    const __amdgpu_buffer_rsrc_t ares = make_rsrc((const uint16_t*)a.x + (int64_t)m0 * K, (uint32_t)(vrows * K * 2));
+    const __amdgpu_buffer_rsrc_t bres = make_rsrc((const uint16_t*)a.w + (int64_t)g * K * N, (uint32_t)(K * N * 2));
+    uint32_t aoff[2], boff[2];
+    int arow[2], akc[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = tid + 256 * i;
+        arow[i] = c >> 2;
+        akc[i] = c & 3;
+        aoff[i] = arow[i] < vrows ? (uint32_t)((arow[i] * K + akc[i] * 8) * 2) : 0x80000000u;
+        if constexpr (TRANS) {
+            // weight [N][K]: like A, rows are output columns
+            const int n = n0 + arow[i];
+            boff[i] = n < N ? (uint32_t)((n * K + akc[i] * 8) * 2) : 0x80000000u;
+        }
+    }
+    // non-transposed weight [K][N]: thread tid takes k rows 2 (tid / 16) and + 1 of n chunk tid % 16
+    const int bkp = tid >> 4, bnc = tid & 15;
+    const bool bn_ok = n0 + bnc * 8 < N;
+    const int nk = (int)((K + GF_BK - 1) / GF_BK);
+
+    uint4 ra[2], rb[2];
+    auto load_stage = [&](int kt) {
+        const int k0 = kt * GF_BK;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const bool kin = k0 + akc[i] * 8 < K;
+            const v4i va = __builtin_amdgcn_raw_buffer_load_b128(ares, kin ? aoff[i] + (uint32_t)(k0 * 2) : 0x80000000u, 0, 0);
+            ra[i] = make_uint4((u32)va[0], (u32)va[1], (u32)va[2], (u32)va[3]);
+        }
+        if constexpr (TRANS) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const bool kin = k0 + akc[i] * 8 < K;
+                const v4i vb = __builtin_amdgcn_raw_buffer_load_b128(bres, kin ? boff[i] + (uint32_t)(k0 * 2) : 0x80000000u, 0, 0);
+                rb[i] = make_uint4((u32)vb[0], (u32)vb[1], (u32)vb[2], (u32)vb[3]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int k = k0 + 2 * bkp + i;
+                const bool ok = k < K && bn_ok;
+                const v4i vb = __builtin_amdgcn_raw_buffer_load_b128(
+                    bres, ok ? (uint32_t)((k * N + n0 + bnc * 8) * 2) : 0x80000000u, 0, 0);
+                rb[i] = make_uint4((u32)vb[0], (u32)vb[1], (u32)vb[2], (u32)vb[3]);
+            }
+        }
+    };
+    auto store_stage = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            *reinterpret_cast<uint4*>(&As[buf][arow[i] * GF_PITCH + akc[i] * 8]) = ra[i];
+        if constexpr (TRANS) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                *reinterpret_cast<uint4*>(&Bs[buf][arow[i] * GF_PITCH + akc[i] * 8]) = rb[i];
+        } else {
+            // 8 columns x 2 consecutive k: one 32-bit (k, k + 1) pair per column
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const u32 lo = comp(rb[0], j >> 1), hi = comp(rb[1], j >> 1);
+                const u32 pair = (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+                *reinterpret_cast<u32*>(&Bs[buf][(bnc * 8 + j) * GF_PITCH + 2 * bkp]) = pair;
+            }
+        }
+    };
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int fm = 0; fm < 2; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < 2; ++fn)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
+
+    load_stage(0);
+    store_stage(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) load_stage(kt + 1);  // in flight during this stage's MFMAs
+#pragma unroll
+        for (int kk = 0; kk < GF_BK / 16; ++kk) {
+            // 32x32x16 operands: lane l holds row / column l % 32, k 8 (l / 32) .. + 7
+            uint4 af[2], bf[2];
+#pragma unroll
+            for (int fm = 0; fm < 2; ++fm)
+                af[fm] = *reinterpret_cast<const uint4*>(
+                    &As[buf][(wm * 64 + fm * 32 + (lane & 31)) * GF_PITCH + kk * 16 + (lane >> 5) * 8]);
+#pragma unroll
+            for (int fn = 0; fn < 2; ++fn)
+                bf[fn] = *reinterpret_cast<const uint4*>(
+                    &Bs[buf][(wn * 64 + fn * 32 + (lane & 31)) * GF_PITCH + kk * 16 + (lane >> 5) * 8]);
+#pragma unroll
+            for (int fm = 0; fm < 2; ++fm)
+#pragma unroll
+                for (int fn = 0; fn < 2; ++fn) {
+                    if constexpr (BF16)
+                        acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                            __builtin_bit_cast(bf16x8, af[fm]), __builtin_bit_cast(bf16x8, bf[fn]), acc[fm][fn], 0, 0, 0);
+                    else
+                        acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            __builtin_bit_cast(f16x8, af[fm]), __builtin_bit_cast(f16x8, bf[fn]), acc[fm][fn], 0, 0, 0);
+                }
+        }
+        if (kt + 1 < nk) store_stage(buf ^ 1);  // the other buffer was last read one stage ago
+        __syncthreads();
+    }
+
+    // Epilogue.  32x32 C layout: lane l holds column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4.
+    uint16_t* y = (uint16_t*)a.y;
+#pragma unroll
+    for (int fn = 0; fn < 2; ++fn) {
+        const int64_t col = n0 + wn * 64 + fn * 32 + (lane & 31);
+        if (col >= N) continue;
+        const float bv = a.bias_dt ? gf_load(a.bias, a.bias_dt, (int64_t)g * N + col) : 0.0f;
+#pragma unroll
+        for (int fm = 0; fm < 2; ++fm)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int lrow = wm * 64 + fm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                if (lrow < vrows) {
+                    const float v = acc[fm][fn][r] + bv;
+                    y[(int64_t)(m0 + lrow) * N + col] = BF16 ? f32_to_bf16_hw(v) : f32_to_f16(v);
+                }
+            }
+    }
+}
+
+// Any dtype and layout: one output element per thread iteration (grid-stride), fp32 accumulation
+// in k order, the bias added in fp32, one narrowing to the output dtype.
+__global__ __launch_bounds__(256) void gmm_generic_kernel(const GmmFArgs a)
+{
+    const int64_t total = a.M * a.N;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int row = (int)(i / a.N);
+        const int64_t col = i % a.N;
+        const int g = group_of_row(a.gt, row);
+        const int64_t wb = (int64_t)g * a.K * a.N;
+        float acc = 0.0f;
+        for (int64_t k = 0; k < a.K; ++k) {
+            const float xv = gf_load(a.x, a.x_dt, (int64_t)row * a.K + k);
+            const float wv = gf_load(a.w, a.x_dt, wb + (a.trans ? col * a.K + k : k * a.N + col));
+            acc = acc + xv * wv;
+        }
+        if (a.bias_dt) acc = acc + gf_load(a.bias, a.bias_dt, (int64_t)g * a.N + col);
+        gf_store(a.y, a.x_dt, i, acc);
+    }
+}
+
+}  // namespace cb
+
+using namespace cb;
+
+// The reference's launch_gmm (grouped_matmul_launch.h:66-70) with the plugin's checks
+// (grouped_matmul_plugin.cpp:127-157, in order) moved behind a status return.  K = 0 writes the
+// bias (or zeros).
+extern "C" int cb_grouped_matmul(const void* x, const void* weight, const void* bias, int x_dtype, int bias_dtype,
+                                 const int64_t* group_list, int64_t group_len, int64_t M, int64_t K, int64_t N,
+                                 int64_t E, int transpose_weight, void* y, void* stream)
+{
+    if (M < 0 || K < 0 || N < 0 || E < 0) return CB_ERR_SHAPE;
+    if (E < 1 || E > kGmmMaxExperts) return CB_ERR_GROUP_COUNT;  // plugin :138-139
+    if (x_dtype != CB_DT_FLOAT16 && x_dtype != CB_DT_BFLOAT16 && x_dtype != CB_DT_FLOAT32) return CB_ERR_DTYPE;
+    if (bias && bias_dtype != CB_DT_FLOAT16 && bias_dtype != CB_DT_BFLOAT16 && bias_dtype != CB_DT_FLOAT32)
+        return CB_ERR_DTYPE;
+    const int vs = validate_group_list(group_list, group_len, E, M);
+    if (vs != CB_OK) return vs;
+    if (M == 0 || N == 0) return CB_OK;
+    if (!x && K > 0) return CB_ERR_NULL_POINTER;
+    if ((!weight && K > 0) || !y) return CB_ERR_NULL_POINTER;
+    if (M > 0x7fffffffLL) return CB_ERR_SHAPE;
+
+    GmmFArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.x = x;
+    a.w = weight;
+    a.bias = bias;
+    a.y = y;
+    a.M = M;
+    a.K = K;
+    a.N = N;
+    a.x_dt = x_dtype;
+    a.bias_dt = bias ? bias_dtype : 0;
+    a.trans = transpose_weight ? 1 : 0;
+    hipStream_t st = (hipStream_t)stream;
+    TimedLaunch timed(st);
+
+    const bool mfma = x_dtype != CB_DT_FLOAT32 && K > 0 && K % 8 == 0 && N % 8 == 0 && aligned(x, 16) &&
+                      aligned(weight, 16) && K * N * 2 < (1LL << 31) && GF_BM * K * 2 < (1LL << 31);
+    if (mfma) {
+        build_group_table(a.gt, group_list, E, GF_BM);
+        a.ntiles = (int)((N + GF_BN - 1) / GF_BN);
+        const int64_t blocks = (int64_t)a.gt.total_mtiles * a.ntiles;
+        if (blocks <= 0) return CB_OK;
+        const dim3 grid((unsigned)blocks);
+        const bool bf = x_dtype == CB_DT_BFLOAT16;
+        if (bf && a.trans) hipLaunchKernelGGL((gmm_mfma_kernel<true, true>), grid, dim3(256), 0, st, a);
+        else if (bf) hipLaunchKernelGGL((gmm_mfma_kernel<true, false>), grid, dim3(256), 0, st, a);
+        else if (a.trans) hipLaunchKernelGGL((gmm_mfma_kernel<false, true>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((gmm_mfma_kernel<false, false>), grid, dim3(256), 0, st, a);
+        return check_launch();
+    }
+    build_group_table(a.gt, group_list, E, 1);
+    const int64_t total = M * N;
+    const int64_t blocks = (total + 255) / 256;
+    hipLaunchKernelGGL(gmm_generic_kernel, dim3((unsigned)(blocks < 65536 ? blocks : 65536)), dim3(256), 0, st, a);
+    return check_launch();
+}

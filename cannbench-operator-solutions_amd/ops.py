@@ -11,6 +11,7 @@ Reference plugins mirrored (paths under operators/):
   dynamic_quant                dynamicquant/csrc/ops/dynamic_quant/op_plugin/dynamic_quant_plugin.cpp:30-87
   grouped_matmul_swiglu_quant  groupedmatmulswigluquant/csrc/ops/grouped_matmul_swiglu_quant/op_plugin/gmsq_plugin.cpp:40-145
   quant_matmul                 quantmatmul/csrc/ops/quant_matmul/op_plugin/quant_matmul_plugin.cpp:48-267
+  grouped_matmul               groupedmatmul/csrc/ops/grouped_matmul/op_plugin/grouped_matmul_plugin.cpp:38-185
   grouped_matmul_quant         (no reference op) group semantics of groupedmatmul/csrc/ops/grouped_matmul/op_plugin/grouped_matmul_plugin.cpp:42-185
   moe_re_routing               moererouting/csrc/ops/moe_re_routing/op_plugin/moe_re_routing_plugin.cpp:33-161
   moe_finalize_routing         moefinalizerouting/csrc/ops/moe_finalize_routing/op_plugin/moe_finalize_routing_plugin.cpp:31-230
@@ -274,6 +275,82 @@ def quant_matmul(x1, x2, scale, *, offset=None, pertoken_scale=None, bias=None, 
         _ptr(x1), _ptr(x2), _ptr(scale), _dtype_code(scale.dtype), scale.numel(),
         _ptr(offset), off_n, _ptr(pertoken_scale), pt_n, _ptr(bias), bias_dt, bias_n, bias_batched,
         batch, M, K, N, _dtype_code(out.dtype), _ptr(out), _stream())
+    _raise_status(name, rc)
+    return out
+
+
+# ------------------------------------------------------------------------------------------------
+# GroupedMatmul (float)
+# ------------------------------------------------------------------------------------------------
+_GMM_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+
+def _gmm_ends(group_list, E, M):
+    ends = [int(v) for v in group_list]
+    prev = 0
+    for v in ends:
+        _check(v >= prev, "grouped_matmul: group_list must be a non-decreasing cumsum")
+        _check(v <= M, "grouped_matmul: group_list values must not exceed M")
+        prev = v
+    _check(prev == M, "grouped_matmul: group_list[-1] must equal M")
+    return ends
+
+
+def _gmm_outputs(y, ends, split_item):
+    """split_item 0/1: one view per expert along M; 2/3: the joined [M, N] tensor
+    (grouped_matmul_plugin.cpp:61-77)."""
+    if split_item in (0, 1):
+        out, s = [], 0
+        for e in ends:
+            out.append(y.narrow(0, s, e - s))
+            s = e
+        return out
+    return [y]
+
+
+def grouped_matmul_meta(x, weight, group_list, bias=None, split_item=0, transpose_weight=False):
+    _check(x.dim() == 2, "grouped_matmul: x must be 2D [M, K]")
+    _check(weight.dim() == 3, "grouped_matmul: weight must be 3D [E, K, N] or [E, N, K]")
+    M, E = x.size(0), weight.size(0)
+    N = weight.size(1) if transpose_weight else weight.size(2)
+    _check(len(group_list) == E, "grouped_matmul: group_list length must equal the number of experts")
+    ends = _gmm_ends(group_list, E, M)
+    y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    return _gmm_outputs(y, ends, split_item)
+
+
+def grouped_matmul(x, weight, group_list, bias=None, split_item=0, transpose_weight=False):
+    """y[rows_g] = x[rows_g] @ weight[g] (+ bias[g]) per expert g, in the dtype of x (fp16, bf16 or
+    fp32); weight [E, K, N], or [E, N, K] with transpose_weight.  Returns a list: one view per expert
+    (split_item 0 / 1) or the joined [M, N] tensor (2 / 3)."""
+    name = "grouped_matmul"
+    _check(x.dim() == 2, f"{name}: x must be 2D [M, K]")
+    _check(weight.dim() == 3, f"{name}: weight must be 3D [E, K, N] or [E, N, K]")
+    x = x.contiguous()
+    weight = weight.contiguous()
+    M, K = x.shape
+    E = weight.size(0)
+    _check(E >= 1, f"{name}: weight must contain at least one expert")
+    _check(E <= L.CB_GMM_MAX_EXPERTS, f"{name}: at most {L.CB_GMM_MAX_EXPERTS} experts are supported")
+    _check(len(group_list) == E, f"{name}: group_list length must equal the number of experts")
+    N = weight.size(1) if transpose_weight else weight.size(2)
+    k_stored = weight.size(2) if transpose_weight else weight.size(1)
+    _check(k_stored == K, f"{name}: K dimension mismatch between x and weight")
+    ends = _gmm_ends(group_list, E, M)
+    if bias is not None:
+        bias = bias.contiguous()
+        _check(bias.numel() == E * N, f"{name}: bias must have shape [E, N]")
+    _check(x.dtype in _GMM_DTYPES and weight.dtype == x.dtype, f"{name}: unsupported dtype")
+    _check(bias is None or bias.dtype in _GMM_DTYPES, f"{name}: unsupported dtype")
+    y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    out = _gmm_outputs(y, ends, split_item)
+    if M == 0 or N == 0:
+        return out
+    _on_device(name, x, weight, bias)
+    gla = L.int64_array(ends)
+    rc = L.load().cb_grouped_matmul(
+        _ptr(x), _ptr(weight), _ptr(bias), _dtype_code(x.dtype), _dtype_code(bias.dtype) if bias is not None else 0,
+        gla, len(ends), M, K, N, E, 1 if transpose_weight else 0, _ptr(y), _stream())
     _raise_status(name, rc)
     return out
 

@@ -20,6 +20,8 @@ SCHEMAS = {
         "grouped_matmul_swiglu_quant(Tensor x, Tensor weight, Tensor weight_scale, Tensor x_scale, int[] group_list) -> (Tensor y, Tensor y_scale)",
     "quant_matmul":
         "quant_matmul(Tensor x1, Tensor x2, Tensor scale, *, Tensor? offset=None, Tensor? pertoken_scale=None, Tensor? bias=None, str? output_dtype=None) -> Tensor",
+    "grouped_matmul":
+        "grouped_matmul(Tensor x, Tensor weight, int[] group_list, Tensor? bias=None, int split_item=0, bool transpose_weight=False) -> Tensor[]",
     "grouped_matmul_quant":
         "grouped_matmul_quant(Tensor x, Tensor weight, Tensor weight_scale, Tensor x_scale, int[] group_list) -> Tensor",
     "moe_re_routing":
@@ -39,6 +41,7 @@ _IMPLS = {
     "quant_matmul": (ops.quant_matmul,
                      lambda x1, x2, scale, *, offset=None, pertoken_scale=None, bias=None, output_dtype=None:
                      ops.quant_matmul_meta(x1, x2, scale, offset, pertoken_scale, bias, output_dtype)),
+    "grouped_matmul": (ops.grouped_matmul, ops.grouped_matmul_meta),
     "grouped_matmul_quant": (ops.grouped_matmul_quant, ops.grouped_matmul_quant_meta),
     "moe_re_routing": (ops.moe_re_routing, ops.moe_re_routing_meta),
     "moe_finalize_routing": (ops.moe_finalize_routing, ops.moe_finalize_routing_meta),

@@ -204,6 +204,21 @@ int cb_grouped_matmul_quant(const int8_t* x, const int8_t* weight, const float* 
                             int64_t M, int64_t K, int64_t N, int64_t E, void* out, void* stream);
 
 /*
+ * GroupedMatmul, the float grouped GEMM: y[rows_g, :] = x[rows_g, :] @ weight[g] (+ bias[g, :]).
+ * Replaces launch_gmm(x, w, b, y, ws, M, N, K, GmmGroupArg, xDtype, biasDtype, hasBias, transB,
+ * stream) (operators/groupedmatmul/csrc/ops/grouped_matmul/op_kernel/grouped_matmul_launch.h:66-70)
+ * with the plugin's checks (op_plugin/grouped_matmul_plugin.cpp:127-157) as status codes; no
+ * workspace.  x_dtype and bias_dtype are CB_DT_FLOAT16 / CB_DT_BFLOAT16 / CB_DT_FLOAT32 (bias may be
+ * NULL); at most 64 experts (GMM_MAX_E).
+ *   x [M, K], weight [E, K, N] (transpose_weight = 0) or [E, N, K] (1), bias [E, N], y [M, N] in x_dtype
+ * Accumulation in fp32, the bias added in fp32, one round-to-nearest-even narrowing.  K = 0 writes
+ * the bias (or zeros).
+ */
+int cb_grouped_matmul(const void* x, const void* weight, const void* bias, int x_dtype, int bias_dtype,
+                      const int64_t* group_list, int64_t group_len, int64_t M, int64_t K, int64_t N,
+                      int64_t E, int transpose_weight, void* y, void* stream);
+
+/*
  * Raw grouped int8 GEMM with exact int32 accumulation: c[rows_g, :] = x[rows_g, :] @ weight[g].
  * Replaces the reference's first GroupedMatmulSwigluQuant stage launch_gmsq_cube(x, w, c, ws, M, K,
  * N, E, GmsqGroupArg, stream) (op_kernel/gmsq_launch.h:67-69, gmsq_cube_kernel.cpp:15-16), which

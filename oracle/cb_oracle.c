@@ -17,6 +17,8 @@
  *   or_grouped_matmul_quant  group routing of operators/groupedmatmul/.../op_plugin/grouped_matmul_plugin.cpp:82-95
  *                      with the QuantMatmul epilogue order (no reference op exists: parity unpinned by the
  *                      reference, pinned here only by the closed forms the tests check)
+ *   or_grouped_matmul  operators/groupedmatmul/csrc/ops/grouped_matmul/op_plugin/grouped_matmul_plugin.cpp:14-17
+ *                      and op_kernel/grouped_matmul_kernel.cpp:15-17,111-150 (float GEMM per expert + bias)
  *   or_moe_re_routing        operators/moererouting/.../op_kernel/moe_re_routing_kernel.cpp:15-24
  *   or_moe_finalize_routing  operators/moefinalizerouting/.../op_kernel/moe_finalize_routing_kernel.cpp:14-25,137-183
  *   or_dequant_swiglu_quant  operators/dequantswigluquant/.../op_kernel/dqsq_kernel.cpp:15-27,334-427,476-524
@@ -334,6 +336,40 @@ void or_grouped_matmul_quant(const int8_t* x, const int8_t* w, const float* ws, 
 /* ============================================================================================
  * Routing operators on either side of the expert FFN.
  * ============================================================================================ */
+
+/* GroupedMatmul (grouped_matmul_plugin.cpp:14-17, grouped_matmul_kernel.cpp:111-150): for the rows
+ * of expert g, y = x @ w[g] (+ bias[g]).  The reference accumulates on its matrix unit in fp32 in an
+ * order of its own; this restatement accumulates in double (the exact sum up to double rounding),
+ * adds the bias in double, then narrows double -> fp32 -> the output dtype (RNE), so a GPU result
+ * within the fp32 accumulation error of the exact sum agrees to one output ulp.
+ * Elements: fp16 / bf16 as uint16 bits, fp32 as float; w [E, K, N] or, with trans, [E, N, K]. */
+static inline double gload(const void* p, int dt, int64_t i)
+{
+    if (dt == DT_F32) return (double)((const float*)p)[i];
+    return (double)load16((const uint16_t*)p, i, dt);
+}
+
+void or_grouped_matmul(const void* x, const void* w, const void* bias, int x_dt, int bias_dt, const int64_t* gl,
+                       int64_t E, int64_t M, int64_t K, int64_t N, int trans, void* y)
+{
+    (void)M; /* the rows are gl[E - 1] == M */
+    for (int64_t g = 0; g < E; ++g) {
+        const int64_t r0 = g ? gl[g - 1] : 0, r1 = gl[g];
+        const int64_t wb = g * K * N;
+#pragma omp parallel for schedule(static)
+        for (int64_t r = r0; r < r1; ++r) {
+            for (int64_t n = 0; n < N; ++n) {
+                double acc = 0.0;
+                for (int64_t k = 0; k < K; ++k)
+                    acc += gload(x, x_dt, r * K + k) * gload(w, x_dt, wb + (trans ? n * K + k : k * N + n));
+                if (bias) acc += gload(bias, bias_dt, g * N + n);
+                const float f = (float)acc;
+                if (x_dt == DT_F32) ((float*)y)[r * N + n] = f;
+                else ((uint16_t*)y)[r * N + n] = store16(f, x_dt);
+            }
+        }
+    }
+}
 
 /* MoeReRouting (operators/moererouting/csrc/ops/moe_re_routing/op_kernel/moe_re_routing_kernel.cpp:15-24):
  * the (rank i, expert j) cell's cnt[i][j] rows move from source offset

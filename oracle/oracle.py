@@ -36,6 +36,7 @@ def lib():
         L.or_gmsq.argtypes = [P, P, P, P, P, I64, I64, I64, I64, I64, I64, P, P]
         L.or_quant_matmul.argtypes = [P, P, P, I, I64, P, I64, P, I64, P, I, I64, I, I64, I64, I64, I64, I, P, I64, I64]
         L.or_grouped_matmul_quant.argtypes = [P, P, P, P, P, I64, I64, I64, I64, I64, I64, P]
+        L.or_grouped_matmul.argtypes = [P, P, P, I, I, P, I64, I64, I64, I64, I, P]
         L.or_moe_re_routing.argtypes = [P, I64, I64, P, I64, I64, P, P, P, P, P]
         L.or_moe_re_routing.restype = I64
         L.or_moe_finalize_routing.argtypes = [P, I, I64, I64, P, I64, I64, P, P, P, I64, P, I, P, I, P]
@@ -143,6 +144,23 @@ def quant_matmul(x1, x2, scale, scale_dtype="f32", offset=None, pertoken=None, b
                           _p(pt), 0 if pt is None else pt.size, _p(bi), DT[bias_dtype], 0 if bi is None else bi.size,
                           int(bias_batched), batch, M, K, N, DT[out_dtype], _p(out), row_begin, row_end)
     return out
+
+
+def grouped_matmul(x, w, group_list, bias=None, dtype="bf16", bias_dtype=None, trans=False):
+    """GroupedMatmul.  x [M, K], w [E, K, N] (or [E, N, K] with trans), bias [E, N]; 16-bit arrays as
+    uint16 bits (dtype 'bf16' / 'f16'), fp32 as float32.  Returns y [M, N] in the same form."""
+    et = np.float32 if dtype == "f32" else np.uint16
+    x = _c(x, et)
+    w = _c(w, et)
+    M, K = x.shape
+    E = w.shape[0]
+    N = w.shape[1] if trans else w.shape[2]
+    bdt = bias_dtype or dtype
+    b = None if bias is None else _c(bias, np.float32 if bdt == "f32" else np.uint16)
+    gl = _c(group_list, np.int64)
+    y = np.zeros((M, N), et)
+    lib().or_grouped_matmul(_p(x), _p(w), _p(b), DT[dtype], DT[bdt], _p(gl), E, M, K, N, 1 if trans else 0, _p(y))
+    return y
 
 
 def grouped_matmul_quant(x, w, ws, xs, group_list, row_begin=0, row_end=None):

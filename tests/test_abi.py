@@ -155,6 +155,24 @@ def test_routing_validation(lib):
     assert so.cb_moe_gating_top_k_softmax(FAKE, 3, 0, 8, None, 2, FAKE, FAKE, FAKE, None) == L.CB_ERR_EMPTY
 
 
+def test_grouped_matmul_validation(lib):
+    L, so = lib
+    gl = lambda v: L.int64_array(v)
+    # E outside [1, 64], dtype, group_list checks, then empty shapes return before any device use
+    assert so.cb_grouped_matmul(FAKE, FAKE, None, 3, 0, gl([]), 0, 4, 8, 8, 0, 0, FAKE, None) == L.CB_ERR_GROUP_COUNT
+    assert so.cb_grouped_matmul(FAKE, FAKE, None, 3, 0, gl([4] * 65), 65, 4, 8, 8, 65, 0, FAKE, None) \
+        == L.CB_ERR_GROUP_COUNT
+    assert so.cb_grouped_matmul(FAKE, FAKE, None, 4, 0, gl([4]), 1, 4, 8, 8, 1, 0, FAKE, None) == L.CB_ERR_DTYPE
+    assert so.cb_grouped_matmul(FAKE, FAKE, FAKE, 2, 5, gl([4]), 1, 4, 8, 8, 1, 0, FAKE, None) == L.CB_ERR_DTYPE
+    assert so.cb_grouped_matmul(FAKE, FAKE, None, 2, 0, gl([4]), 1, 4, 8, 8, 2, 0, FAKE, None) == L.CB_ERR_GROUP_LEN
+    assert so.cb_grouped_matmul(FAKE, FAKE, None, 2, 0, gl([3, 2]), 2, 4, 8, 8, 2, 0, FAKE, None) \
+        == L.CB_ERR_GROUP_ORDER
+    assert so.cb_grouped_matmul(FAKE, FAKE, None, 2, 0, gl([1, 3]), 2, 4, 8, 8, 2, 0, FAKE, None) \
+        == L.CB_ERR_GROUP_TOTAL
+    assert so.cb_grouped_matmul(None, None, None, 1, 0, gl([0]), 1, 0, 8, 8, 1, 0, None, None) == L.CB_OK
+    assert so.cb_grouped_matmul(FAKE, FAKE, None, 1, 0, gl([4]), 1, 4, 8, 8, 1, 0, None, None) == L.CB_ERR_NULL_POINTER
+
+
 def test_launch_grid_limits(lib):
     """Row counts whose one-block-per-row launch would exceed the dispatch's 32-bit work-item count
     are rejected before any device call; the same operators accept them below the limit (checked on

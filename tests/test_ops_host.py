@@ -134,3 +134,35 @@ def test_routing_checks_and_meta(cb):
     assert y.shape == (5, 32) and y.dtype == torch.int8 and s.shape == (5,)
     y, ei, ri = torch.ops.cann_bench.moe_gating_top_k_softmax(torch.empty(2, 7, 64, device=m), None, 8)
     assert y.shape == (2, 7, 8) and ei.dtype == torch.int32 and ri.dtype == torch.int32
+
+
+def test_grouped_matmul_checks_and_outputs(cb):
+    """The float GroupedMatmul mirror: the plugin's checks with its messages, split_item views, and
+    no CPU fallback once the checks pass (grouped_matmul_plugin.cpp:61-77, 127-157)."""
+    f = torch.float32
+    x, w = torch.zeros(5, 8, dtype=f), torch.zeros(2, 8, 3, dtype=f)
+    with pytest.raises(RuntimeError, match="at least one expert"):
+        cb.grouped_matmul(x, torch.zeros(0, 8, 3, dtype=f), [])
+    with pytest.raises(RuntimeError, match="at most 64 experts"):
+        cb.grouped_matmul(x, torch.zeros(65, 8, 3, dtype=f), [5] * 65)
+    with pytest.raises(RuntimeError, match="group_list length must equal"):
+        cb.grouped_matmul(x, w, [5])
+    with pytest.raises(RuntimeError, match="K dimension mismatch"):
+        cb.grouped_matmul(x, torch.zeros(2, 7, 3, dtype=f), [2, 5])
+    with pytest.raises(RuntimeError, match="non-decreasing"):
+        cb.grouped_matmul(x, w, [3, 2])
+    with pytest.raises(RuntimeError, match=r"group_list\[-1\] must equal M"):
+        cb.grouped_matmul(x, w, [2, 4])
+    with pytest.raises(RuntimeError, match=r"bias must have shape \[E, N\]"):
+        cb.grouped_matmul(x, w, [2, 5], bias=torch.zeros(5))
+    with pytest.raises(RuntimeError, match="unsupported dtype"):
+        cb.grouped_matmul(x.to(torch.int8), w.to(torch.int8), [2, 5])
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        cb.grouped_matmul(x, w, [2, 5])
+    # empty outputs return before any device access; split_item 0/1 give per-expert views
+    outs = cb.grouped_matmul(torch.zeros(0, 8, dtype=f), w, [0, 0])
+    assert len(outs) == 2 and all(o.shape == (0, 3) for o in outs)
+    outs = cb.grouped_matmul(torch.zeros(0, 8, dtype=f), w, [0, 0], split_item=2)
+    assert len(outs) == 1 and outs[0].shape == (0, 3)
+    views = cb.ops.grouped_matmul_meta(x, torch.zeros(2, 3, 8, dtype=f), [2, 5], transpose_weight=True)
+    assert [v.shape for v in views] == [(2, 3), (3, 3)]

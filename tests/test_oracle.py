@@ -346,3 +346,71 @@ def test_golden_grouped_matmul_quant(orc):
     g = _golden("grouped_matmul_quant")
     out = orc.grouped_matmul_quant(g["x"], g["w"], g["ws"], g["xs"], g["group_list"])
     np.testing.assert_array_equal(out, g["out"])
+
+
+# ---------------------------------------------------------------------------------------------
+# GroupedMatmul (float)
+# ---------------------------------------------------------------------------------------------
+def _gmm_np(x, w, ends, bias, trans):
+    """float64 numpy product per expert (a library matmul, not the oracle's loop)."""
+    y = np.zeros((x.shape[0], w.shape[1] if trans else w.shape[2]))
+    s = 0
+    for g, e in enumerate(ends):
+        wg = w[g].T if trans else w[g]
+        y[s:e] = x[s:e] @ wg + (0.0 if bias is None else bias[g])
+        s = e
+    return y
+
+
+@pytest.mark.parametrize("trans", [False, True])
+def test_grouped_matmul_f32_against_numpy(orc, trans):
+    rng = np.random.default_rng(3)
+    counts = [7, 0, 30, 1]
+    M, K, N, E = sum(counts), 40, 24, len(counts)
+    ends = np.cumsum(counts)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = rng.standard_normal((E, N, K) if trans else (E, K, N)).astype(np.float32)
+    b = rng.standard_normal((E, N)).astype(np.float32)
+    y = orc.grouped_matmul(x, w, ends, b, dtype="f32", trans=trans)
+    ref = _gmm_np(x.astype(np.float64), w.astype(np.float64), ends, b.astype(np.float64), trans)
+    np.testing.assert_allclose(y, ref, rtol=1e-6, atol=1e-5)
+    # the transposed layout of the same weights gives the same result
+    wt = np.ascontiguousarray(np.swapaxes(w, 1, 2))
+    np.testing.assert_array_equal(orc.grouped_matmul(x, wt, ends, b, dtype="f32", trans=not trans), y)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("bias_dtype", [None, "f32", "bf16"])
+def test_grouped_matmul_16bit_rounding(orc, dtype, bias_dtype):
+    """16-bit inputs: the output is the float64 product narrowed to fp32 then to the dtype (torch's
+    RNE), and a swapped expert or a dropped bias is detected."""
+    rng = np.random.default_rng(4)
+    counts = [12, 3, 0, 17]
+    M, K, N, E = sum(counts), 64, 40, len(counts)
+    ends = np.cumsum(counts)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    xt = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(tdt)
+    wt = torch.from_numpy(rng.standard_normal((E, K, N)).astype(np.float32)).to(tdt)
+    bits = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)
+    bt, bb = None, None
+    if bias_dtype == "f32":
+        bt = torch.from_numpy(rng.standard_normal((E, N)).astype(np.float32))
+        bb = bt.numpy()
+    elif bias_dtype == "bf16":
+        bt = torch.from_numpy(rng.standard_normal((E, N)).astype(np.float32)).to(torch.bfloat16)
+        bb = bits(bt)
+    y = orc.grouped_matmul(bits(xt), bits(wt), ends, bb, dtype=dtype, bias_dtype=bias_dtype)
+    ref = _gmm_np(xt.double().numpy(), wt.double().numpy(), ends, None if bt is None else bt.double().numpy(), False)
+    ref_bits = bits(torch.from_numpy(ref.astype(np.float32)).to(tdt))
+    d = np.abs(y.astype(np.int32) - ref_bits.astype(np.int32))
+    assert d.max() <= 1 and (d > 0).mean() < 0.01
+    # an expert swap moves the rows of the swapped groups by far more than one ulp
+    ends_sw = ends.copy()
+    y_sw = orc.grouped_matmul(bits(xt), bits(wt[[1, 0, 2, 3]]), ends_sw, bb, dtype=dtype, bias_dtype=bias_dtype)
+    assert (np.abs(y_sw[:15].astype(np.int32) - y[:15].astype(np.int32)) > 1).mean() > 0.5
+
+
+def test_grouped_matmul_k0_gives_bias(orc):
+    b = np.arange(6, dtype=np.float32).reshape(2, 3)
+    y = orc.grouped_matmul(np.zeros((3, 0), np.float32), np.zeros((2, 0, 3), np.float32), [1, 3], b, dtype="f32")
+    np.testing.assert_array_equal(y, np.stack([b[0], b[1], b[1]]))
