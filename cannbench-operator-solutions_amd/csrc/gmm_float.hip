@@ -20,8 +20,15 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kGmmMaxExperts = 64;  // GMM_MAX_E (grouped_matmul_launch.h)
-constexpr int GF_BM = 128, GF_BN = 128, GF_BK = 32;
-constexpr int GF_PITCH = GF_BK + 8;  // elements per LDS row (80 B): a 16-lane b128 read phase hits 16 bank groups
+#ifndef CB_GMM_BK
+#define CB_GMM_BK 32
+#endif
+constexpr int GF_BM = 128, GF_BN = 128, GF_BK = CB_GMM_BK;
+// elements per LDS row (BK + 8: 80 B at BK 32): a 16-lane b128 read phase hits 16 distinct bank groups
+constexpr int GF_PITCH = GF_BK + 8;
+constexpr int GF_KCH = GF_BK / 8;                       // 16-byte chunks per row and stage
+constexpr int GF_CA = GF_BM * GF_KCH / 256;             // A (and [N][K] weight) chunks per thread
+constexpr int GF_CP = (GF_BK / 2) * (GF_BN / 8) / 256;  // [K][N] weight: (k, k + 1) chunk pairs per thread
 
 struct GmmFArgs {
     const void* x;
@@ -76,16 +83,16 @@ __global__ __launch_bounds__(256, 2) void gmm_mfma_kernel(const GmmFArgs a)
     const int wm = wave >> 1, wn = wave & 1;
 
     // Operand streams through buffer resources (offsets outside a resource read zeros).
-    // A: rows [m0, r1) of x; thread chunks c = tid + 256 i: row c / 4, k chunk c % 4 (8 elements).
+    // A: rows [m0, r1) of x; thread chunks c = tid + 256 i: row c / KCH, k chunk c % KCH (8 elements).
     const __amdgpu_buffer_rsrc_t ares = make_rsrc((const uint16_t*)a.x + (int64_t)m0 * K, (uint32_t)(vrows * K * 2));
     const __amdgpu_buffer_rsrc_t bres = make_rsrc((const uint16_t*)a.w + (int64_t)g * K * N, (uint32_t)(K * N * 2));
-    uint32_t aoff[2], boff[2];
-    int arow[2], akc[2];
+    uint32_t aoff[GF_CA], boff[GF_CA];
+    int arow[GF_CA], akc[GF_CA];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < GF_CA; ++i) {
         const int c = tid + 256 * i;
-        arow[i] = c >> 2;
-        akc[i] = c & 3;
+        arow[i] = c / GF_KCH;
+        akc[i] = c % GF_KCH;
         aoff[i] = arow[i] < vrows ? (uint32_t)((arow[i] * K + akc[i] * 8) * 2) : 0x80000000u;
         if constexpr (TRANS) {
             // weight [N][K]: like A, rows are output columns
@@ -93,54 +100,60 @@ __global__ __launch_bounds__(256, 2) void gmm_mfma_kernel(const GmmFArgs a)
             boff[i] = n < N ? (uint32_t)((n * K + akc[i] * 8) * 2) : 0x80000000u;
         }
     }
-    // non-transposed weight [K][N]: thread tid takes k rows 2 (tid / 16) and + 1 of n chunk tid % 16
-    const int bkp = tid >> 4, bnc = tid & 15;
-    const bool bn_ok = n0 + bnc * 8 < N;
+    // weight [K][N]: pair p = tid + 256 i takes k rows 2 (p / 16) and + 1 of n chunk p % 16
+    int bkp[GF_CP], bnc[GF_CP];
+    bool bn_ok[GF_CP];
+#pragma unroll
+    for (int i = 0; i < GF_CP; ++i) {
+        const int p2 = tid + 256 * i;
+        bkp[i] = p2 >> 4;
+        bnc[i] = p2 & 15;
+        bn_ok[i] = n0 + bnc[i] * 8 < N;
+    }
     const int nk = (int)((K + GF_BK - 1) / GF_BK);
 
-    uint4 ra[2], rb[2];
+    uint4 ra[GF_CA], rb[2 * GF_CP > GF_CA ? 2 * GF_CP : GF_CA];
+    auto ld16 = [](__amdgpu_buffer_rsrc_t r, uint32_t off) {
+        const v4i v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+        return make_uint4((u32)v[0], (u32)v[1], (u32)v[2], (u32)v[3]);
+    };
     auto load_stage = [&](int kt) {
         const int k0 = kt * GF_BK;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const bool kin = k0 + akc[i] * 8 < K;
-            const v4i va = __builtin_amdgcn_raw_buffer_load_b128(ares, kin ? aoff[i] + (uint32_t)(k0 * 2) : 0x80000000u, 0, 0);
-            ra[i] = make_uint4((u32)va[0], (u32)va[1], (u32)va[2], (u32)va[3]);
-        }
+        for (int i = 0; i < GF_CA; ++i)
+            ra[i] = ld16(ares, k0 + akc[i] * 8 < K ? aoff[i] + (uint32_t)(k0 * 2) : 0x80000000u);
         if constexpr (TRANS) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const bool kin = k0 + akc[i] * 8 < K;
-                const v4i vb = __builtin_amdgcn_raw_buffer_load_b128(bres, kin ? boff[i] + (uint32_t)(k0 * 2) : 0x80000000u, 0, 0);
-                rb[i] = make_uint4((u32)vb[0], (u32)vb[1], (u32)vb[2], (u32)vb[3]);
-            }
+            for (int i = 0; i < GF_CA; ++i)
+                rb[i] = ld16(bres, k0 + akc[i] * 8 < K ? boff[i] + (uint32_t)(k0 * 2) : 0x80000000u);
         } else {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int k = k0 + 2 * bkp + i;
-                const bool ok = k < K && bn_ok;
-                const v4i vb = __builtin_amdgcn_raw_buffer_load_b128(
-                    bres, ok ? (uint32_t)((k * N + n0 + bnc * 8) * 2) : 0x80000000u, 0, 0);
-                rb[i] = make_uint4((u32)vb[0], (u32)vb[1], (u32)vb[2], (u32)vb[3]);
-            }
+            for (int i = 0; i < GF_CP; ++i)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int k = k0 + 2 * bkp[i] + h;
+                    rb[2 * i + h] = ld16(bres, k < K && bn_ok[i] ? (uint32_t)((k * N + n0 + bnc[i] * 8) * 2) : 0x80000000u);
+                }
         }
     };
     auto store_stage = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < GF_CA; ++i)
             *reinterpret_cast<uint4*>(&As[buf][arow[i] * GF_PITCH + akc[i] * 8]) = ra[i];
         if constexpr (TRANS) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < GF_CA; ++i)
                 *reinterpret_cast<uint4*>(&Bs[buf][arow[i] * GF_PITCH + akc[i] * 8]) = rb[i];
         } else {
             // 8 columns x 2 consecutive k: one 32-bit (k, k + 1) pair per column
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const u32 lo = comp(rb[0], j >> 1), hi = comp(rb[1], j >> 1);
-                const u32 pair = (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-                *reinterpret_cast<u32*>(&Bs[buf][(bnc * 8 + j) * GF_PITCH + 2 * bkp]) = pair;
-            }
+            for (int i = 0; i < GF_CP; ++i)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const u32 lo = comp(rb[2 * i], j >> 1), hi = comp(rb[2 * i + 1], j >> 1);
+                    const u32 pair = (j & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+                    *reinterpret_cast<u32*>(&Bs[buf][(bnc[i] * 8 + j) * GF_PITCH + 2 * bkp[i]]) = pair;
+                }
         }
     };
 
