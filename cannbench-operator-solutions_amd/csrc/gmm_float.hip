@@ -23,12 +23,10 @@ constexpr int kGmmMaxExperts = 64;  // GMM_MAX_E (grouped_matmul_launch.h)
 #ifndef CB_GMM_BK
 #define CB_GMM_BK 32
 #endif
-constexpr int GF_BM = 128, GF_BN = 128, GF_BK = CB_GMM_BK;
+constexpr int GF_BK = CB_GMM_BK;
 // elements per LDS row (BK + 8: 80 B at BK 32): a 16-lane b128 read phase hits 16 distinct bank groups
 constexpr int GF_PITCH = GF_BK + 8;
-constexpr int GF_KCH = GF_BK / 8;                       // 16-byte chunks per row and stage
-constexpr int GF_CA = GF_BM * GF_KCH / 256;             // A (and [N][K] weight) chunks per thread
-constexpr int GF_CP = (GF_BK / 2) * (GF_BN / 8) / 256;  // [K][N] weight: (k, k + 1) chunk pairs per thread
+constexpr int GF_KCH = GF_BK / 8;  // 16-byte chunks per row and stage
 
 struct GmmFArgs {
     const void* x;
@@ -55,10 +53,18 @@ __device__ __forceinline__ void gf_store(void* p, int dt, int64_t i, float v)
     else ((uint16_t*)p)[i] = f32_to_f16(v);
 }
 
-// One 128 x 128 tile per workgroup: pid -> (row tile, column tile) with 4 row tiles per column sweep.
-template <bool BF16, bool TRANS>
-__global__ __launch_bounds__(256, 2) void gmm_mfma_kernel(const GmmFArgs a)
+// One BM x BN tile per workgroup of WM x WN waves (wave tiles (BM / WM) x (BN / WN)): pid -> (row
+// tile, column tile) with 4 row tiles per column sweep.  Launched as 128 x 128 with 2 x 2 waves.
+template <bool BF16, bool TRANS, int GF_BM, int GF_BN, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN, 64 * WM * WN > 256 ? 1 : 2) void gmm_mfma_kernel(const GmmFArgs a)
 {
+    constexpr int NT = 64 * WM * WN;
+    constexpr int TM = GF_BM / WM, TN = GF_BN / WN, FM = TM / 32, FN = TN / 32;
+    constexpr int GF_CA = GF_BM * GF_KCH / NT;             // A chunks per thread
+    constexpr int GF_CB = GF_BN * GF_KCH / NT;             // [N][K] weight chunks per thread
+    constexpr int GF_CP = (GF_BK / 2) * (GF_BN / 8) / NT;  // [K][N] weight: (k, k + 1) chunk pairs per thread
+    constexpr int NCH = GF_BN / 8;                         // 8-column chunks per weight row
+    static_assert(GF_CA >= 1 && GF_CB >= 1 && GF_CP >= 1, "tile too small for the workgroup");
     __shared__ __attribute__((aligned(16))) uint16_t As[2][GF_BM * GF_PITCH];
     __shared__ __attribute__((aligned(16))) uint16_t Bs[2][GF_BN * GF_PITCH];  // [n][k]
 
@@ -80,39 +86,43 @@ __global__ __launch_bounds__(256, 2) void gmm_mfma_kernel(const GmmFArgs a)
     const int64_t K = a.K, N = a.N;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
 
     // Operand streams through buffer resources (offsets outside a resource read zeros).
     // A: rows [m0, r1) of x; thread chunks c = tid + 256 i: row c / KCH, k chunk c % KCH (8 elements).
     const __amdgpu_buffer_rsrc_t ares = make_rsrc((const uint16_t*)a.x + (int64_t)m0 * K, (uint32_t)(vrows * K * 2));
     const __amdgpu_buffer_rsrc_t bres = make_rsrc((const uint16_t*)a.w + (int64_t)g * K * N, (uint32_t)(K * N * 2));
-    uint32_t aoff[GF_CA], boff[GF_CA];
-    int arow[GF_CA], akc[GF_CA];
+    uint32_t aoff[GF_CA], boff[GF_CB];
+    int arow[GF_CA], akc[GF_CA], brow[GF_CB], bkc[GF_CB];
 #pragma unroll
     for (int i = 0; i < GF_CA; ++i) {
-        const int c = tid + 256 * i;
+        const int c = tid + NT * i;
         arow[i] = c / GF_KCH;
         akc[i] = c % GF_KCH;
         aoff[i] = arow[i] < vrows ? (uint32_t)((arow[i] * K + akc[i] * 8) * 2) : 0x80000000u;
-        if constexpr (TRANS) {
-            // weight [N][K]: like A, rows are output columns
-            const int n = n0 + arow[i];
-            boff[i] = n < N ? (uint32_t)((n * K + akc[i] * 8) * 2) : 0x80000000u;
-        }
     }
-    // weight [K][N]: pair p = tid + 256 i takes k rows 2 (p / 16) and + 1 of n chunk p % 16
+#pragma unroll
+    for (int i = 0; i < GF_CB; ++i) {
+        // weight [N][K]: like A, rows are output columns
+        const int c = tid + NT * i;
+        brow[i] = c / GF_KCH;
+        bkc[i] = c % GF_KCH;
+        const int n = n0 + brow[i];
+        boff[i] = n < N ? (uint32_t)((n * K + bkc[i] * 8) * 2) : 0x80000000u;
+    }
+    // weight [K][N]: pair p = tid + NT i takes k rows 2 (p / NCH) and + 1 of n chunk p % NCH
     int bkp[GF_CP], bnc[GF_CP];
     bool bn_ok[GF_CP];
 #pragma unroll
     for (int i = 0; i < GF_CP; ++i) {
-        const int p2 = tid + 256 * i;
-        bkp[i] = p2 >> 4;
-        bnc[i] = p2 & 15;
+        const int p2 = tid + NT * i;
+        bkp[i] = p2 / NCH;
+        bnc[i] = p2 % NCH;
         bn_ok[i] = n0 + bnc[i] * 8 < N;
     }
     const int nk = (int)((K + GF_BK - 1) / GF_BK);
 
-    uint4 ra[GF_CA], rb[2 * GF_CP > GF_CA ? 2 * GF_CP : GF_CA];
+    uint4 ra[GF_CA], rb[TRANS ? GF_CB : 2 * GF_CP];
     auto ld16 = [](__amdgpu_buffer_rsrc_t r, uint32_t off) {
         const v4i v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
         return make_uint4((u32)v[0], (u32)v[1], (u32)v[2], (u32)v[3]);
@@ -124,8 +134,8 @@ __global__ __launch_bounds__(256, 2) void gmm_mfma_kernel(const GmmFArgs a)
             ra[i] = ld16(ares, k0 + akc[i] * 8 < K ? aoff[i] + (uint32_t)(k0 * 2) : 0x80000000u);
         if constexpr (TRANS) {
 #pragma unroll
-            for (int i = 0; i < GF_CA; ++i)
-                rb[i] = ld16(bres, k0 + akc[i] * 8 < K ? boff[i] + (uint32_t)(k0 * 2) : 0x80000000u);
+            for (int i = 0; i < GF_CB; ++i)
+                rb[i] = ld16(bres, k0 + bkc[i] * 8 < K ? boff[i] + (uint32_t)(k0 * 2) : 0x80000000u);
         } else {
 #pragma unroll
             for (int i = 0; i < GF_CP; ++i)
@@ -142,8 +152,8 @@ __global__ __launch_bounds__(256, 2) void gmm_mfma_kernel(const GmmFArgs a)
             *reinterpret_cast<uint4*>(&As[buf][arow[i] * GF_PITCH + akc[i] * 8]) = ra[i];
         if constexpr (TRANS) {
 #pragma unroll
-            for (int i = 0; i < GF_CA; ++i)
-                *reinterpret_cast<uint4*>(&Bs[buf][arow[i] * GF_PITCH + akc[i] * 8]) = rb[i];
+            for (int i = 0; i < GF_CB; ++i)
+                *reinterpret_cast<uint4*>(&Bs[buf][brow[i] * GF_PITCH + bkc[i] * 8]) = rb[i];
         } else {
             // 8 columns x 2 consecutive k: one 32-bit (k, k + 1) pair per column
 #pragma unroll
@@ -157,11 +167,11 @@ __global__ __launch_bounds__(256, 2) void gmm_mfma_kernel(const GmmFArgs a)
         }
     };
 
-    f32x16 acc[2][2];
+    f32x16 acc[FM][FN];
 #pragma unroll
-    for (int fm = 0; fm < 2; ++fm)
+    for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-        for (int fn = 0; fn < 2; ++fn)
+        for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
 
@@ -174,19 +184,19 @@ __global__ __launch_bounds__(256, 2) void gmm_mfma_kernel(const GmmFArgs a)
 #pragma unroll
         for (int kk = 0; kk < GF_BK / 16; ++kk) {
             // 32x32x16 operands: lane l holds row / column l % 32, k 8 (l / 32) .. + 7
-            uint4 af[2], bf[2];
+            uint4 af[FM], bf[FN];
 #pragma unroll
-            for (int fm = 0; fm < 2; ++fm)
+            for (int fm = 0; fm < FM; ++fm)
                 af[fm] = *reinterpret_cast<const uint4*>(
-                    &As[buf][(wm * 64 + fm * 32 + (lane & 31)) * GF_PITCH + kk * 16 + (lane >> 5) * 8]);
+                    &As[buf][(wm * TM + fm * 32 + (lane & 31)) * GF_PITCH + kk * 16 + (lane >> 5) * 8]);
 #pragma unroll
-            for (int fn = 0; fn < 2; ++fn)
+            for (int fn = 0; fn < FN; ++fn)
                 bf[fn] = *reinterpret_cast<const uint4*>(
-                    &Bs[buf][(wn * 64 + fn * 32 + (lane & 31)) * GF_PITCH + kk * 16 + (lane >> 5) * 8]);
+                    &Bs[buf][(wn * TN + fn * 32 + (lane & 31)) * GF_PITCH + kk * 16 + (lane >> 5) * 8]);
 #pragma unroll
-            for (int fm = 0; fm < 2; ++fm)
+            for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-                for (int fn = 0; fn < 2; ++fn) {
+                for (int fn = 0; fn < FN; ++fn) {
                     if constexpr (BF16)
                         acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                             __builtin_bit_cast(bf16x8, af[fm]), __builtin_bit_cast(bf16x8, bf[fn]), acc[fm][fn], 0, 0, 0);
@@ -202,15 +212,15 @@ __global__ __launch_bounds__(256, 2) void gmm_mfma_kernel(const GmmFArgs a)
     // Epilogue.  32x32 C layout: lane l holds column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4.
     uint16_t* y = (uint16_t*)a.y;
 #pragma unroll
-    for (int fn = 0; fn < 2; ++fn) {
-        const int64_t col = n0 + wn * 64 + fn * 32 + (lane & 31);
+    for (int fn = 0; fn < FN; ++fn) {
+        const int64_t col = n0 + wn * TN + fn * 32 + (lane & 31);
         if (col >= N) continue;
         const float bv = a.bias_dt ? gf_load(a.bias, a.bias_dt, (int64_t)g * N + col) : 0.0f;
 #pragma unroll
-        for (int fm = 0; fm < 2; ++fm)
+        for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int lrow = wm * 64 + fm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                const int lrow = wm * TM + fm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
                 if (lrow < vrows) {
                     const float v = acc[fm][fn][r] + bv;
                     y[(int64_t)(m0 + lrow) * N + col] = BF16 ? f32_to_bf16_hw(v) : f32_to_f16(v);
@@ -279,18 +289,18 @@ extern "C" int cb_grouped_matmul(const void* x, const void* weight, const void* 
     TimedLaunch timed(st);
 
     const bool mfma = x_dtype != CB_DT_FLOAT32 && K > 0 && K % 8 == 0 && N % 8 == 0 && aligned(x, 16) &&
-                      aligned(weight, 16) && K * N * 2 < (1LL << 31) && GF_BM * K * 2 < (1LL << 31);
+                      aligned(weight, 16) && K * N * 2 < (1LL << 31) && 128 * K * 2 < (1LL << 31);
     if (mfma) {
-        build_group_table(a.gt, group_list, E, GF_BM);
-        a.ntiles = (int)((N + GF_BN - 1) / GF_BN);
+        build_group_table(a.gt, group_list, E, 128);
+        a.ntiles = (int)((N + 127) / 128);
         const int64_t blocks = (int64_t)a.gt.total_mtiles * a.ntiles;
         if (blocks <= 0) return CB_OK;
         const dim3 grid((unsigned)blocks);
         const bool bf = x_dtype == CB_DT_BFLOAT16;
-        if (bf && a.trans) hipLaunchKernelGGL((gmm_mfma_kernel<true, true>), grid, dim3(256), 0, st, a);
-        else if (bf) hipLaunchKernelGGL((gmm_mfma_kernel<true, false>), grid, dim3(256), 0, st, a);
-        else if (a.trans) hipLaunchKernelGGL((gmm_mfma_kernel<false, true>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((gmm_mfma_kernel<false, false>), grid, dim3(256), 0, st, a);
+        if (bf && a.trans) hipLaunchKernelGGL((gmm_mfma_kernel<true, true, 128, 128, 2, 2>), grid, dim3(256), 0, st, a);
+        else if (bf) hipLaunchKernelGGL((gmm_mfma_kernel<true, false, 128, 128, 2, 2>), grid, dim3(256), 0, st, a);
+        else if (a.trans) hipLaunchKernelGGL((gmm_mfma_kernel<false, true, 128, 128, 2, 2>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((gmm_mfma_kernel<false, false, 128, 128, 2, 2>), grid, dim3(256), 0, st, a);
         return check_launch();
     }
     build_group_table(a.gt, group_list, E, 1);

@@ -108,3 +108,16 @@ def test_grouped_matmul_torch_op(cb):
     y1 = torch.ops.cann_bench.grouped_matmul(x.to(DEV), w.to(DEV), ends, b.to(DEV), 2, False)
     y2 = cb.grouped_matmul(x.to(DEV), w.to(DEV), ends, bias=b.to(DEV), split_item=2)
     assert torch.equal(y1[0], y2[0])
+
+
+@pytest.mark.parametrize("dtype,trans", [("bf16", False), ("bf16", True), ("f16", False)])
+def test_grouped_matmul_many_tiles(cb, orc, dtype, trans):
+    """A larger ragged problem: 29 row tiles of 128 (partial ones included) x 32 column tiles, a K
+    tail inside a stage."""
+    counts = [300, 0, 45, 700, 1, 2000, 130]
+    K, N = 264, 4096
+    x, w, b, ends = _inputs(counts, K, N, dtype, trans, "f32", 77)
+    y = cb.grouped_matmul(x.to(DEV), w.to(DEV), ends, bias=b.to(DEV), split_item=2, transpose_weight=trans)[0]
+    ref = orc.grouped_matmul(host(x, dtype), host(w, dtype), ends, b.numpy(), dtype=dtype, bias_dtype="f32",
+                             trans=trans)
+    _check(y, ref, dtype, x.float(), w.float(), ends, trans)
