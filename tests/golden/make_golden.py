@@ -65,6 +65,16 @@ def main():
     out = orc.grouped_matmul_quant(xd, wd, wsd, xsd, gld)
     np.savez_compressed(os.path.join(HERE, "grouped_matmul_quant.npz"), x=xd, w=wd, ws=wsd, xs=xsd,
                         group_list=gld, out=out)
+
+    # GroupedMatmul (float): bf16 x [28, 64], w [4, 64, 48], bf16 bias, an empty group
+    rg = np.random.default_rng(2025)
+    counts = np.array([5, 0, 20, 3])
+    gl = np.cumsum(counts).astype(np.int64)
+    xg = bf16_bits(rg.standard_normal((int(gl[-1]), 64)).astype(np.float32))
+    wg = bf16_bits(rg.standard_normal((4, 64, 48)).astype(np.float32))
+    bg = bf16_bits(rg.standard_normal((4, 48)).astype(np.float32))
+    yg = orc.grouped_matmul(xg, wg, gl, bg, dtype="bf16", bias_dtype="bf16")
+    np.savez_compressed(os.path.join(HERE, "grouped_matmul.npz"), x=xg, w=wg, bias=bg, group_list=gl, y=yg)
     print("wrote fixtures to", HERE)
 
 

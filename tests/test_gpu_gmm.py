@@ -121,3 +121,15 @@ def test_grouped_matmul_many_tiles(cb, orc, dtype, trans):
     ref = orc.grouped_matmul(host(x, dtype), host(w, dtype), ends, b.numpy(), dtype=dtype, bias_dtype="f32",
                              trans=trans)
     _check(y, ref, dtype, x.float(), w.float(), ends, trans)
+
+
+def test_grouped_matmul_golden_fixture(cb):
+    """The committed fixture (tests/golden/grouped_matmul.npz, bf16 with a bf16 bias and an empty
+    group), within the same bar."""
+    import os
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "grouped_matmul.npz"), allow_pickle=False)
+    as_t = lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16)
+    x, w, b = as_t(g["x"]), as_t(g["w"]), as_t(g["bias"])
+    ends = g["group_list"].tolist()
+    y = cb.grouped_matmul(x.to(DEV), w.to(DEV), ends, bias=b.to(DEV), split_item=2)[0]
+    _check(y, g["y"], "bf16", x.float(), w.float(), ends, False)

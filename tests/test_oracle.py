@@ -342,6 +342,12 @@ def test_golden_quant_matmul(orc):
     np.testing.assert_array_equal(out, g["out"])
 
 
+def test_golden_grouped_matmul(orc):
+    g = _golden("grouped_matmul")
+    y = orc.grouped_matmul(g["x"], g["w"], g["group_list"], g["bias"], dtype="bf16", bias_dtype="bf16")
+    np.testing.assert_array_equal(y, g["y"])
+
+
 def test_golden_grouped_matmul_quant(orc):
     g = _golden("grouped_matmul_quant")
     out = orc.grouped_matmul_quant(g["x"], g["w"], g["ws"], g["xs"], g["group_list"])
