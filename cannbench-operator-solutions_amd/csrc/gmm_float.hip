@@ -10,14 +10,18 @@
 // in fp32, one round-to-nearest-even narrowing.  fp32 inputs and shapes off the vector path
 // (K or N not a multiple of 8, misaligned operands, 32-bit offsets exceeded) take a plain fp32 loop.
 #include <cstring>
+#include <mutex>
+#include <set>
+#include <utility>
 
-#include "gemm_i8.hpp"
+#include "gemm_lds.hpp"
 
 namespace cb {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
 
 constexpr int kGmmMaxExperts = 64;  // GMM_MAX_E (grouped_matmul_launch.h)
 #ifndef CB_GMM_BK
@@ -90,7 +94,8 @@ __global__ __launch_bounds__(64 * WM * WN, 64 * WM * WN > 256 ? 1 : 2) void gmm_
 
     // Operand streams through buffer resources (offsets outside a resource read zeros).
     // A: rows [m0, r1) of x; thread chunks c = tid + 256 i: row c / KCH, k chunk c % KCH (8 elements).
-    const __amdgpu_buffer_rsrc_t ares = make_rsrc((const uint16_t*)a.x + (int64_t)m0 * K, (uint32_t)(vrows * K * 2));
+    const __amdgpu_buffer_rsrc_t ares = make_rsrc((const uint16_t*)a.x + (int64_t)m0 * K,
+                                                     (uint32_t)((vrows < GF_BM ? vrows : GF_BM) * K * 2));
     const __amdgpu_buffer_rsrc_t bres = make_rsrc((const uint16_t*)a.w + (int64_t)g * K * N, (uint32_t)(K * N * 2));
     uint32_t aoff[GF_CA], boff[GF_CB];
     int arow[GF_CA], akc[GF_CA], brow[GF_CB], bkc[GF_CB];
@@ -229,6 +234,179 @@ __global__ __launch_bounds__(64 * WM * WN, 64 * WM * WN > 256 ? 1 : 2) void gmm_
     }
 }
 
+// 256 x 256 tiles on the int8 LDS core's structure: 8 waves (4 x 2) of 64 x 128, 64-deep stages
+// (128 bytes of every operand row) DMA'd from global memory straight into a 2-stage LDS ring
+// (buffer_load ... lds), one stage in flight while the other is multiplied.
+//   x rows and a [N][K] weight: K-contiguous rows of 128 bytes, 16-byte chunks XOR-swizzled by
+//   (row >> 1) & 7 (as the int8 core's A), fragments read with ds_read_b128.
+//   a [K][N] weight: 64 rows of 256 columns (512 bytes), 16-byte chunks XOR-swizzled by 2 (k % 4);
+//   fragments read with ds_read_b64_tr_b16: in each 16-lane group, lane s addresses row
+//   k0 + s / 4, columns nb + 4 (s % 4) .. + 3, and lane j receives k0 .. k0 + 3 of column nb + j.
+// Chunks past K or N point outside their buffer resource and read zeros.
+constexpr int GL_BM = 256, GL_BN = 256, GL_BK = 64, GL_WN = 2, GL_NT = 512;  // 4 x 2 waves
+constexpr int GL_ROWB = GL_BK * 2;                 // bytes per K-contiguous row and stage
+constexpr int GL_A_BYTES = GL_BM * GL_ROWB;        // 32 KB
+constexpr int GL_B_BYTES = GL_BN * GL_ROWB;        // 32 KB either layout
+constexpr int GL_STAGE = GL_A_BYTES + GL_B_BYTES;
+constexpr int GL_ISSUE = (GL_A_BYTES + GL_B_BYTES) / 16 / GL_NT;  // DMAs per thread per stage (8)
+
+__device__ __forceinline__ int gl_swz(int r) { return (r >> 1) & 7; }
+
+template <bool BF16, bool TRANS>
+__global__ __launch_bounds__(GL_NT, 1) void gmm_lds_kernel(const GmmFArgs a)
+{
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    constexpr int GROUP_M = 4;
+    const int pid = blockIdx.x;
+    const int T_m = a.gt.total_mtiles, T_n = a.ntiles;
+    const int per_group = GROUP_M * T_n;
+    const int first_m = (pid / per_group) * GROUP_M;
+    const int gsz = (T_m - first_m) < GROUP_M ? (T_m - first_m) : GROUP_M;
+    const int mt = first_m + (pid % per_group) % gsz;
+    const int nt = (pid % per_group) / gsz;
+    const int g = group_of_tile(a.gt, mt);
+    const int rs = g ? a.gt.row_end[g - 1] : 0;
+    const int r1 = a.gt.row_end[g];
+    const int m0 = rs + (mt - a.gt.tile_start[g]) * GL_BM;
+    const int vrows = r1 - m0;
+    const int n0 = nt * GL_BN;
+    const int64_t K = a.K, N = a.N;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / GL_WN, wn = wave % GL_WN;
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(CB_LDS uint8_t*)smem;
+
+    const __amdgpu_buffer_rsrc_t ares = make_rsrc((const uint16_t*)a.x + (int64_t)m0 * K,
+                                                     (uint32_t)((vrows < GL_BM ? vrows : GL_BM) * K * 2));
+    const __amdgpu_buffer_rsrc_t bres = make_rsrc((const uint16_t*)a.w + (int64_t)g * K * N, (uint32_t)(K * N * 2));
+    // per DMA i: the element offset of the chunk at k = 0 (or -1: nothing to fetch) and its k start
+    int64_t aoff[4], boff[4];
+    int akq[4], bk[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int cid = (i * 8 + wave) * 64 + lane;  // lane-linear 16-byte chunk of the stage
+        const int row = cid >> 3, pos = cid & 7;
+        const int q = pos ^ gl_swz(row);
+        akq[i] = q * 8;
+        aoff[i] = row < vrows ? (int64_t)row * K + q * 8 : -1;
+        if constexpr (TRANS) {
+            bk[i] = q * 8;
+            boff[i] = n0 + row < N ? (int64_t)(n0 + row) * K + q * 8 : -1;
+        } else {
+            const int krow = cid >> 5, cpos = cid & 31;
+            const int c = cpos ^ (2 * (krow & 3));  // logical 8-column chunk
+            bk[i] = krow;
+            boff[i] = n0 + c * 8 < N ? (int64_t)krow * N + n0 + c * 8 : -1;
+        }
+    }
+    const int nk = (int)((K + GL_BK - 1) / GL_BK);
+    auto issue = [&](int kt) {
+        const uint32_t sa = lds_base + (uint32_t)((kt & 1) * GL_STAGE);
+        const int k0 = kt * GL_BK;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const bool ok = aoff[i] >= 0 && k0 + akq[i] < K;
+            dma16(ares, ok ? (uint32_t)((aoff[i] + k0) * 2) : 0x80000000u,
+                  __builtin_amdgcn_readfirstlane(sa + (uint32_t)((i * 8 + wave) * 1024)));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            bool ok;
+            int64_t off;
+            if constexpr (TRANS) {
+                ok = boff[i] >= 0 && k0 + bk[i] < K;
+                off = boff[i] + k0;
+            } else {
+                ok = boff[i] >= 0 && k0 + bk[i] < K;
+                off = boff[i] + (int64_t)k0 * N;
+            }
+            dma16(bres, ok ? (uint32_t)(off * 2) : 0x80000000u,
+                  __builtin_amdgcn_readfirstlane(sa + GL_A_BYTES + (uint32_t)((i * 8 + wave) * 1024)));
+        }
+    };
+
+    f32x16 acc[2][4];
+#pragma unroll
+    for (int fm = 0; fm < 2; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < 4; ++fn)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0.0f;
+
+    issue(0);
+    issue(1);
+    for (int kt = 0; kt < nk; ++kt) {
+        wait_vmcnt_barrier<GL_ISSUE>();  // stage kt has landed (stage kt + 1 may stay in flight)
+        const CB_LDS uint8_t* st = (const CB_LDS uint8_t*)smem + (kt & 1) * GL_STAGE;
+#pragma unroll
+        for (int ks = 0; ks < GL_BK / 16; ++ks) {
+            uint4 af[2], bfr[4];
+            const int q = 2 * ks + (lane >> 5);
+#pragma unroll
+            for (int fm = 0; fm < 2; ++fm) {
+                const int r = wm * 64 + fm * 32 + (lane & 31);
+                af[fm] = __builtin_bit_cast(uint4, *(const CB_LDS v4i*)(st + r * GL_ROWB + ((q ^ gl_swz(r)) << 4)));
+            }
+#pragma unroll
+            for (int fn = 0; fn < 4; ++fn) {
+                if constexpr (TRANS) {
+                    const int r = wn * 128 + fn * 32 + (lane & 31);
+                    bfr[fn] = __builtin_bit_cast(uint4, *(const CB_LDS v4i*)(st + GL_A_BYTES + r * GL_ROWB + ((q ^ gl_swz(r)) << 4)));
+                } else {
+                    const int grp = lane >> 4, s = lane & 15;
+                    const int nb = wn * 128 + fn * 32 + 16 * (grp & 1);
+                    const int col = nb + 4 * (s & 3);
+                    u32 w[4];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const int k = ks * 16 + 8 * (grp >> 1) + 4 * h + (s >> 2);
+                        const int chunk = (col >> 3) ^ (2 * (k & 3));
+                        const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (CB_LDS v4i16*)(st + GL_A_BYTES + k * (GL_BN * 2) + chunk * 16 + (col & 7) * 2));
+                        w[2 * h] = (u32)(uint16_t)v[0] | ((u32)(uint16_t)v[1] << 16);
+                        w[2 * h + 1] = (u32)(uint16_t)v[2] | ((u32)(uint16_t)v[3] << 16);
+                    }
+                    bfr[fn] = make_uint4(w[0], w[1], w[2], w[3]);
+                }
+            }
+#pragma unroll
+            for (int fm = 0; fm < 2; ++fm)
+#pragma unroll
+                for (int fn = 0; fn < 4; ++fn) {
+                    if constexpr (BF16)
+                        acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                            __builtin_bit_cast(bf16x8, af[fm]), __builtin_bit_cast(bf16x8, bfr[fn]), acc[fm][fn], 0, 0, 0);
+                    else
+                        acc[fm][fn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            __builtin_bit_cast(f16x8, af[fm]), __builtin_bit_cast(f16x8, bfr[fn]), acc[fm][fn], 0, 0, 0);
+                }
+        }
+        // every wave is done with this buffer before the DMA of stage kt + 2 overwrites it
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        issue(kt + 2);  // past K: fetches nothing
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // Epilogue.  32x32 C layout: lane l holds column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4.
+    uint16_t* y = (uint16_t*)a.y;
+#pragma unroll
+    for (int fn = 0; fn < 4; ++fn) {
+        const int64_t col = n0 + wn * 128 + fn * 32 + (lane & 31);
+        if (col >= N) continue;
+        const float bv = a.bias_dt ? gf_load(a.bias, a.bias_dt, (int64_t)g * N + col) : 0.0f;
+#pragma unroll
+        for (int fm = 0; fm < 2; ++fm)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int lrow = wm * 64 + fm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                if (lrow < vrows) {
+                    const float v = acc[fm][fn][r] + bv;
+                    y[(int64_t)(m0 + lrow) * N + col] = BF16 ? f32_to_bf16_hw(v) : f32_to_f16(v);
+                }
+            }
+    }
+}
+
 // Any dtype and layout: one output element per thread iteration (grid-stride), fp32 accumulation
 // in k order, the bias added in fp32, one narrowing to the output dtype.
 __global__ __launch_bounds__(256) void gmm_generic_kernel(const GmmFArgs a)
@@ -248,6 +426,23 @@ __global__ __launch_bounds__(256) void gmm_generic_kernel(const GmmFArgs a)
         if (a.bias_dt) acc = acc + gf_load(a.bias, a.bias_dt, (int64_t)g * a.N + col);
         gf_store(a.y, a.x_dt, i, acc);
     }
+}
+
+#ifndef CB_GMM_LDS
+#define CB_GMM_LDS 1
+#endif
+constexpr bool kGmmLds = CB_GMM_LDS;
+
+// Raise a kernel's dynamic LDS limit once per (kernel, device).
+static void set_dynamic_lds_once(const void* kern, int bytes)
+{
+    static std::mutex mu;
+    static std::set<std::pair<const void*, int>> done;
+    int dev = -1;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lock(mu);
+    if (done.insert({kern, dev}).second)
+        (void)hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
 }
 
 }  // namespace cb
@@ -291,6 +486,21 @@ extern "C" int cb_grouped_matmul(const void* x, const void* weight, const void* 
     const bool mfma = x_dtype != CB_DT_FLOAT32 && K > 0 && K % 8 == 0 && N % 8 == 0 && aligned(x, 16) &&
                       aligned(weight, 16) && K * N * 2 < (1LL << 31) && 128 * K * 2 < (1LL << 31);
     if (mfma) {
+        if (kGmmLds && 256 * K * 2 < (1LL << 31)) {
+            build_group_table(a.gt, group_list, E, GL_BM);
+            a.ntiles = (int)((N + GL_BN - 1) / GL_BN);
+            const int64_t blocks = (int64_t)a.gt.total_mtiles * a.ntiles;
+            if (blocks <= 0) return CB_OK;
+            const bool bf = x_dtype == CB_DT_BFLOAT16;
+            const void* kern = bf ? (a.trans ? (const void*)gmm_lds_kernel<true, true> : (const void*)gmm_lds_kernel<true, false>)
+                                  : (a.trans ? (const void*)gmm_lds_kernel<false, true> : (const void*)gmm_lds_kernel<false, false>);
+            set_dynamic_lds_once(kern, 2 * GL_STAGE);
+            if (bf && a.trans) hipLaunchKernelGGL((gmm_lds_kernel<true, true>), dim3((unsigned)blocks), dim3(GL_NT), 2 * GL_STAGE, st, a);
+            else if (bf) hipLaunchKernelGGL((gmm_lds_kernel<true, false>), dim3((unsigned)blocks), dim3(GL_NT), 2 * GL_STAGE, st, a);
+            else if (a.trans) hipLaunchKernelGGL((gmm_lds_kernel<false, true>), dim3((unsigned)blocks), dim3(GL_NT), 2 * GL_STAGE, st, a);
+            else hipLaunchKernelGGL((gmm_lds_kernel<false, false>), dim3((unsigned)blocks), dim3(GL_NT), 2 * GL_STAGE, st, a);
+            return check_launch();
+        }
         build_group_table(a.gt, group_list, E, 128);
         a.ntiles = (int)((N + 127) / 128);
         const int64_t blocks = (int64_t)a.gt.total_mtiles * a.ntiles;
