@@ -231,8 +231,17 @@ def bench_gmm(steps, warmup, dev):
     timer = KernelTimer(steps)
     ms = time_op(fn, steps, warmup, timer)
     kms = timer.mean_ms()
+    # the same problem with the weight stored [E, N, K] (transpose_weight), and the vendor batched
+    # bf16 GEMM (torch.bmm -> hipBLASLt, no bias) on the equal-sized groups, wall-clock timed
+    wt = w.transpose(1, 2).contiguous()
+    ms_t = time_op(lambda: cb.grouped_matmul(x, wt, gl, bias=b, split_item=2, transpose_weight=True), steps, warmup)
+    del wt
+    xb = x.view(E, rows, K)
+    ms_v = time_op(lambda: torch.bmm(xb, w), steps, warmup)
     return {"value": round(flops / (ms * 1e-3) / 1e12, 1), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
             "kernel_ms": round(kms, 4),
+            "transpose_weight_tflops": round(flops / (ms_t * 1e-3) / 1e12, 1),
+            "vendor_bmm_tflops": round(flops / (ms_v * 1e-3) / 1e12, 1),
             "roofline": roofline("mfma", flops / (kms * 1e-3) / 1e12, "TFLOP/s", peak=PEAK_BF16_TFLOPS),
             "config": {"workload": "grouped_matmul", "dtype": "bf16", "experts": E, "rows_per_expert": rows,
                        "K": K, "N": N, "bias": "bf16", "transpose_weight": False}}

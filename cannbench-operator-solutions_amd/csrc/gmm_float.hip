@@ -9,6 +9,7 @@
 // transposed on its way into LDS when it arrives N-contiguous), fp32 accumulation, the bias added
 // in fp32, one round-to-nearest-even narrowing.  fp32 inputs and shapes off the vector path
 // (K or N not a multiple of 8, misaligned operands, 32-bit offsets exceeded) take a plain fp32 loop.
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <set>
@@ -428,10 +429,13 @@ __global__ __launch_bounds__(256) void gmm_generic_kernel(const GmmFArgs a)
     }
 }
 
-#ifndef CB_GMM_LDS
-#define CB_GMM_LDS 1
-#endif
-constexpr bool kGmmLds = CB_GMM_LDS;
+// CANNBENCH_AMD_GMM_TILE=128 selects the 128 x 128 register-staged kernel for every fp16/bf16 shape
+// (it is otherwise taken only where a 256-row block passes 2 GiB); read on every call.
+static bool gmm_lds_enabled()
+{
+    const char* s = std::getenv("CANNBENCH_AMD_GMM_TILE");
+    return !(s && std::atoi(s) == 128);
+}
 
 // Raise a kernel's dynamic LDS limit once per (kernel, device).
 static void set_dynamic_lds_once(const void* kern, int bytes)
@@ -486,7 +490,7 @@ extern "C" int cb_grouped_matmul(const void* x, const void* weight, const void* 
     const bool mfma = x_dtype != CB_DT_FLOAT32 && K > 0 && K % 8 == 0 && N % 8 == 0 && aligned(x, 16) &&
                       aligned(weight, 16) && K * N * 2 < (1LL << 31) && 128 * K * 2 < (1LL << 31);
     if (mfma) {
-        if (kGmmLds && 256 * K * 2 < (1LL << 31)) {
+        if (gmm_lds_enabled() && 256 * K * 2 < (1LL << 31)) {
             build_group_table(a.gt, group_list, E, GL_BM);
             a.ntiles = (int)((N + GL_BN - 1) / GL_BN);
             const int64_t blocks = (int64_t)a.gt.total_mtiles * a.ntiles;

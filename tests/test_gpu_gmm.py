@@ -7,7 +7,7 @@ rounding itself: every element within one output ulp + 1e-6 x sum |x_k w_k|, and
 16-bit outputs differing at all.  fp32 outputs: within 1e-5 relative + 1e-6 x sum |x_k w_k|.
 Shapes cover the MFMA path (K and N multiples of 8: K tails inside a 32-deep stage, partial
 column and row tiles, empty and single-row groups, both weight layouts, every bias dtype) and the
-fp32 loop (fp32 inputs, K or N off the multiple of 8).
+fp32 loop (fp32 inputs, K or N off the multiple of 8).  The MFMA cases run on both tile kernels.
 """
 import numpy as np
 import pytest
@@ -66,10 +66,18 @@ CASES = [
 ]
 
 
+@pytest.fixture(params=["256", "128"])
+def gmm_tile(request, monkeypatch):
+    """The 256 x 256 LDS-DMA kernel (default) and the 128 x 128 register-staged one."""
+    if request.param == "128":
+        monkeypatch.setenv("CANNBENCH_AMD_GMM_TILE", "128")
+    return request.param
+
+
 @pytest.mark.parametrize("counts,K,N", CASES)
 @pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("trans", [False, True])
-def test_grouped_matmul(cb, orc, counts, K, N, dtype, trans):
+def test_grouped_matmul(cb, orc, gmm_tile, counts, K, N, dtype, trans):
     bias_dtype = {"bf16": "f32", "f16": "f16", "f32": "bf16"}[dtype]
     x, w, b, ends = _inputs(counts, K, N, dtype, trans, bias_dtype, K + N + len(counts))
     ys = cb.grouped_matmul(x.to(DEV), w.to(DEV), ends, bias=b.to(DEV), split_item=2, transpose_weight=trans)
@@ -92,7 +100,7 @@ def test_grouped_matmul_no_bias_and_split_views(cb, orc, dtype):
     assert outs[2].data_ptr() == outs[0].data_ptr() + 64 * 256 * 2
 
 
-def test_grouped_matmul_layouts_agree(cb):
+def test_grouped_matmul_layouts_agree(cb, gmm_tile):
     """[E, K, N] and [E, N, K] storage of the same weights give bit-identical results on the MFMA
     path (the same fp32 operation order)."""
     x, w, b, ends = _inputs([90, 170], 96, 256, "bf16", False, "f32", 11)
@@ -111,7 +119,7 @@ def test_grouped_matmul_torch_op(cb):
 
 
 @pytest.mark.parametrize("dtype,trans", [("bf16", False), ("bf16", True), ("f16", False)])
-def test_grouped_matmul_many_tiles(cb, orc, dtype, trans):
+def test_grouped_matmul_many_tiles(cb, orc, gmm_tile, dtype, trans):
     """A larger ragged problem: 29 row tiles of 128 (partial ones included) x 32 column tiles, a K
     tail inside a stage."""
     counts = [300, 0, 45, 700, 1, 2000, 130]
