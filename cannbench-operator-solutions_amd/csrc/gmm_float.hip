@@ -389,23 +389,38 @@ __global__ __launch_bounds__(GL_NT, 1) void gmm_lds_kernel(const GmmFArgs a)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     // Epilogue.  32x32 C layout: lane l holds column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4.
-    uint16_t* y = (uint16_t*)a.y;
+    // Rows r and r + 1 of a lane pair (l, l ^ 1) are swapped so that each lane stores two adjacent
+    // columns of one row as one dword: the even lane row r, columns (c, c + 1), the odd lane row
+    // r + 1, columns (c - 1, c).  Rows past the group's end fall outside the resource and are dropped.
+    const __amdgpu_buffer_rsrc_t ores = make_rsrc((uint16_t*)a.y + (int64_t)m0 * N,
+                                                  (uint32_t)((vrows < GL_BM ? vrows : GL_BM) * N * 2));
+    const bool odd = lane & 1;
+    float bv[4];
+    uint32_t coff[4];
 #pragma unroll
     for (int fn = 0; fn < 4; ++fn) {
         const int64_t col = n0 + wn * 128 + fn * 32 + (lane & 31);
-        if (col >= N) continue;
-        const float bv = a.bias_dt ? gf_load(a.bias, a.bias_dt, (int64_t)g * N + col) : 0.0f;
-#pragma unroll
-        for (int fm = 0; fm < 2; ++fm)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int lrow = wm * 64 + fm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-                if (lrow < vrows) {
-                    const float v = acc[fm][fn][r] + bv;
-                    y[(int64_t)(m0 + lrow) * N + col] = BF16 ? f32_to_bf16_hw(v) : f32_to_f16(v);
-                }
-            }
+        bv[fn] = a.bias_dt ? gf_load(a.bias, a.bias_dt, (int64_t)g * N + (col < N ? col : 0)) : 0.0f;
+        coff[fn] = col < N ? (uint32_t)(col & ~(int64_t)1) * 2u : 0x80000000u;
     }
+#pragma unroll
+    for (int fm = 0; fm < 2; ++fm)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+            const int lrow = wm * 64 + fm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);  // rows lrow, lrow + 1
+            const uint32_t roff = (uint32_t)(lrow + (odd ? 1 : 0)) * (uint32_t)N * 2u;
+#pragma unroll
+            for (int fn = 0; fn < 4; ++fn) {
+                const float v0 = acc[fm][fn][r] + bv[fn], v1 = acc[fm][fn][r + 1] + bv[fn];
+                const uint32_t h0 = BF16 ? f32_to_bf16_hw(v0) : f32_to_f16(v0);
+                const uint32_t h1 = BF16 ? f32_to_bf16_hw(v1) : f32_to_f16(v1);
+                const uint32_t p = h0 | (h1 << 16);
+                // partner lane's pair (quad_perm [1, 0, 3, 2])
+                const uint32_t q = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)p, 0xB1, 0xF, 0xF, false);
+                const uint32_t w = odd ? ((q >> 16) | (p & 0xffff0000u)) : ((p & 0xffffu) | (q << 16));
+                __builtin_amdgcn_raw_buffer_store_b32(w, ores, roff + coff[fn], 0, 0);
+            }
+        }
 }
 
 // Any dtype and layout: one output element per thread iteration (grid-stride), fp32 accumulation
@@ -430,7 +445,7 @@ __global__ __launch_bounds__(256) void gmm_generic_kernel(const GmmFArgs a)
 }
 
 // CANNBENCH_AMD_GMM_TILE=128 selects the 128 x 128 register-staged kernel for every fp16/bf16 shape
-// (it is otherwise taken only where a 256-row block passes 2 GiB); read on every call.
+// (it is otherwise taken only where a 256-row block of x or y passes 2 GiB); read on every call.
 static bool gmm_lds_enabled()
 {
     const char* s = std::getenv("CANNBENCH_AMD_GMM_TILE");
@@ -490,7 +505,7 @@ extern "C" int cb_grouped_matmul(const void* x, const void* weight, const void* 
     const bool mfma = x_dtype != CB_DT_FLOAT32 && K > 0 && K % 8 == 0 && N % 8 == 0 && aligned(x, 16) &&
                       aligned(weight, 16) && K * N * 2 < (1LL << 31) && 128 * K * 2 < (1LL << 31);
     if (mfma) {
-        if (gmm_lds_enabled() && 256 * K * 2 < (1LL << 31)) {
+        if (gmm_lds_enabled() && 256 * K * 2 < (1LL << 31) && 256 * N * 2 < (1LL << 31)) {
             build_group_table(a.gt, group_list, E, GL_BM);
             a.ntiles = (int)((N + GL_BN - 1) / GL_BN);
             const int64_t blocks = (int64_t)a.gt.total_mtiles * a.ntiles;
