@@ -141,3 +141,14 @@ def test_grouped_matmul_golden_fixture(cb):
     ends = g["group_list"].tolist()
     y = cb.grouped_matmul(x.to(DEV), w.to(DEV), ends, bias=b.to(DEV), split_item=2)[0]
     _check(y, g["y"], "bf16", x.float(), w.float(), ends, False)
+
+
+@pytest.mark.parametrize("N", [(1 << 22) - 8, 1 << 22])
+def test_grouped_matmul_wide_n_dispatch(cb, orc, N):
+    """N at the LDS kernel's limit: a 256-row block of y stays under 2 GiB at N = 2^22 - 8 (LDS-DMA
+    kernel) and reaches it at N = 2^22 (128 x 128 kernel); both against the oracle."""
+    counts = [2, 0, 1]
+    x, w, b, ends = _inputs(counts, 8, N, "bf16", False, "f32", 23)
+    y = cb.grouped_matmul(x.to(DEV), w.to(DEV), ends, bias=b.to(DEV), split_item=2)[0]
+    ref = orc.grouped_matmul(host(x, "bf16"), host(w, "bf16"), ends, b.numpy(), dtype="bf16", bias_dtype="f32")
+    _check(y, ref, "bf16", x.float(), w.float(), ends, False)
