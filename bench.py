@@ -135,10 +135,11 @@ def bench_down_prefill(steps, warmup, dev, keep):
     int8 [256, 2048, 7168], bf16 out [131072, 7168]."""
     d = keep["prefill"]
     M = d["x"].shape[0]
-    x = cfgs.rand_i8((M, 2048), dev, 41)
-    xs = cfgs.rand_uniform((M,), 0.005, 0.02, dev, 42)
-    w = cfgs.rand_i8((256, 2048, 7168), dev, 43)
-    ws = cfgs.rand_uniform((256, 7168), 0.001, 0.01, dev, 44)
+    r = cfgs.streams(41, 4)
+    x = cfgs.rand_i8((M, 2048), dev, r[0])
+    xs = cfgs.rand_uniform((M,), 0.005, 0.02, dev, r[1])
+    w = cfgs.rand_i8((256, 2048, 7168), dev, r[2])
+    ws = cfgs.rand_uniform((256, 7168), 0.001, 0.01, dev, r[3])
     ops = 2.0 * M * 2048 * 7168
     fn = lambda: cb.grouped_matmul_quant(x, w, ws, xs, d["group_list"])
     timer = KernelTimer(steps)

@@ -7,8 +7,7 @@ import ctypes
 import os
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
-# CANNBENCH_AMD_LIB points at an alternative build of the same library (kernel tuning sweeps)
-LIB_PATH = os.environ.get("CANNBENCH_AMD_LIB") or os.path.join(PKG_DIR, "libcannbench_amd.so")
+LIB_PATH = os.path.join(PKG_DIR, "libcannbench_amd.so")
 
 # Status codes (cb_status in include/cannbench_amd.h).
 CB_OK = 0
@@ -56,6 +55,7 @@ SIGNATURES = {
     "cb_grouped_matmul_swiglu_quant_workspace_size": (_I64, [_I64, _I64, _I64, _I64]),
     "cb_grouped_matmul_swiglu_quant": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P]),
     "cb_grouped_matmul_swiglu_quant_status": (_I, [_P, _I64, _I64, _I64, _P, _P]),
+    "cb_set_test_overrides": (None, [_I, _I, _I]),
     "cb_grouped_matmul_swiglu_quant_gather": (_I, [_P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P]),
     "cb_quant_matmul": (_I, [_P, _P, _P, _I, _I64, _P, _I64, _P, _I64, _P, _I, _I64, _I, _I64, _I64, _I64, _I64, _I, _P, _P]),
     "cb_grouped_matmul_quant": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P]),

@@ -20,10 +20,11 @@ Routing operators around the experts (a 16384-token prefill batch, top-8 of 256 
     dqsq        DequantSwigluQuant: int32 x [131072, 4096] ~ U{-2^15..2^15}, weight_scale [4096],
                 activation_scale [131072]
 
-Group counts come from numpy (host, exact and portable).  Large tensors are drawn on the device with
-a seeded torch generator (one generator per tensor, seeds in listed order), so every run on the same
-software stack sees identical data; tests that need CPU copies of them copy slices back.
-`scale` < 1 shrinks the row/column counts for quick runs while keeping the group structure.
+Every tensor is drawn on the host with numpy: one numpy.random.default_rng stream per tensor,
+spawned from SeedSequence(seed) in the listed order (so the data does not depend on the torch or
+ROCm version), generated in chunks of at most 256 MiB and copied to the device chunk by chunk.
+Group counts come from numpy.random.default_rng(seed) directly.  `scale` < 1 shrinks the
+row/column counts for quick runs while keeping the group structure.
 """
 import numpy as np
 import torch
@@ -47,23 +48,38 @@ def cumsum_list(counts):
     return [int(v) for v in np.cumsum(counts)]
 
 
-def _gen(device, seed):
-    g = torch.Generator(device=device)
-    g.manual_seed(seed)
-    return g
+_CHUNK = 1 << 28  # host bytes generated per step
 
 
-def rand_i8(shape, device, seed):
-    return torch.randint(-127, 128, shape, dtype=torch.int8, device=device, generator=_gen(device, seed))
+def streams(seed, n):
+    """n independent numpy generators, one per tensor, in the listed order."""
+    return [np.random.default_rng(s) for s in np.random.SeedSequence(seed).spawn(n)]
 
 
-def rand_uniform(shape, lo, hi, device, seed, dtype=torch.float32):
-    t = torch.rand(shape, dtype=torch.float32, device=device, generator=_gen(device, seed))
-    return (t * (hi - lo) + lo).to(dtype)
+def _fill(shape, device, dtype, draw):
+    """A device tensor filled chunk by chunk (along the flattened order) by draw(count) -> ndarray."""
+    out = torch.empty(shape, dtype=dtype, device=device)
+    flat = out.view(-1)
+    per = max(1, _CHUNK // out.element_size())
+    for i in range(0, flat.numel(), per):
+        n = min(per, flat.numel() - i)
+        flat[i:i + n].copy_(torch.from_numpy(np.ascontiguousarray(draw(n))))
+    return out
 
 
-def rand_normal(shape, device, seed, dtype=torch.float32):
-    return torch.randn(shape, dtype=torch.float32, device=device, generator=_gen(device, seed)).to(dtype)
+def rand_i8(shape, device, rng):
+    """int8 uniform over -127..127."""
+    return _fill(shape, device, torch.int8, lambda n: rng.integers(-127, 128, size=n, dtype=np.int8))
+
+
+def rand_uniform(shape, lo, hi, device, rng, dtype=torch.float32):
+    t = _fill(shape, device, torch.float32, lambda n: rng.uniform(lo, hi, size=n).astype(np.float32))
+    return t.to(dtype)
+
+
+def rand_normal(shape, device, rng, dtype=torch.float32):
+    t = _fill(shape, device, torch.float32, lambda n: rng.standard_normal(size=n, dtype=np.float32))
+    return t.to(dtype)
 
 
 def make_dq(device="cuda", rows=1024, cols=4096, seed=0):
@@ -76,33 +92,39 @@ def make_dq(device="cuda", rows=1024, cols=4096, seed=0):
 
 
 def make_ardq(device="cuda", rows=8192, cols=7168, seed=0, dtype=torch.bfloat16):
+    r = streams(seed, 3)
     return {
-        "x1": rand_normal((rows, cols), device, seed + 1, dtype),
-        "x2": rand_normal((rows, cols), device, seed + 2, dtype),
-        "gamma": rand_uniform((cols,), 0.5, 1.5, device, seed + 3, dtype),
+        "x1": rand_normal((rows, cols), device, r[0], dtype),
+        "x2": rand_normal((rows, cols), device, r[1], dtype),
+        "gamma": rand_uniform((cols,), 0.5, 1.5, device, r[2], dtype),
         "epsilon": 1e-6,
     }
 
 
 def make_qmm(device="cuda", M=4096, K=7168, N=4096, seed=0):
+    r = streams(seed, 4)
     return {
-        "x1": rand_i8((M, K), device, seed + 11),
-        "x2": rand_i8((K, N), device, seed + 12),
-        "scale": rand_uniform((N,), 0.001, 0.01, device, seed + 13),
-        "pertoken_scale": rand_uniform((M,), 0.005, 0.02, device, seed + 14),
+        "x1": rand_i8((M, K), device, r[0]),
+        "x2": rand_i8((K, N), device, r[1]),
+        "scale": rand_uniform((N,), 0.001, 0.01, device, r[2]),
+        "pertoken_scale": rand_uniform((M,), 0.005, 0.02, device, r[3]),
         "output_dtype": "bfloat16",
     }
 
 
-def make_gmsq(device="cuda", counts=None, K=7168, N=4096, seed=0):
+def make_gmsq(device="cuda", counts=None, K=7168, N=4096, seed=0, extra=0):
+    """GMSQ inputs; `extra` more generator streams are returned under "rngs" (the decode
+    config's down-projection tensors, drawn after these)."""
     E = len(counts)
     M = int(np.sum(counts))
+    r = streams(seed, 4 + extra)
     return {
-        "x": rand_i8((M, K), device, seed + 21),
-        "weight": rand_i8((E, K, N), device, seed + 22),
-        "weight_scale": rand_uniform((E, N), 0.001, 0.01, device, seed + 23),
-        "x_scale": rand_uniform((M,), 0.005, 0.02, device, seed + 24),
+        "x": rand_i8((M, K), device, r[0]),
+        "weight": rand_i8((E, K, N), device, r[1]),
+        "weight_scale": rand_uniform((E, N), 0.001, 0.01, device, r[2]),
+        "x_scale": rand_uniform((M,), 0.005, 0.02, device, r[3]),
         "group_list": cumsum_list(counts),
+        "rngs": r[4:],
     }
 
 
@@ -113,36 +135,39 @@ def make_gmsq_prefill(device="cuda", scale=1.0, seed=0):
 
 def make_gmsq_decode(device="cuda", seed=0, with_down=True):
     counts = topk_group_counts(256, E_DEFAULT)
-    d = make_gmsq(device, counts, seed=seed)
+    d = make_gmsq(device, counts, seed=seed, extra=2)
     if with_down:
-        d["down_weight"] = rand_i8((E_DEFAULT, 2048, 7168), device, seed + 31)
-        d["down_weight_scale"] = rand_uniform((E_DEFAULT, 7168), 0.001, 0.01, device, seed + 32)
+        r = d["rngs"]
+        d["down_weight"] = rand_i8((E_DEFAULT, 2048, 7168), device, r[0])
+        d["down_weight_scale"] = rand_uniform((E_DEFAULT, 7168), 0.001, 0.01, device, r[1])
     return d
 
 
 def make_gating(device="cuda", tokens=16384, experts=256, k=8, seed=0):
-    return {"x": rand_normal((tokens, experts), device, seed + 1), "k": k}
+    return {"x": rand_normal((tokens, experts), device, streams(seed, 1)[0]), "k": k}
 
 
 def make_rerouting(device="cuda", rows=131072, hidden=7168, ranks=16, experts=16, seed=0):
     rng = np.random.default_rng(seed)
     w = rng.uniform(0.5, 1.5, ranks * experts)
     counts = rng.multinomial(rows, w / w.sum()).reshape(ranks, experts).astype(np.int64)
-    return {"tokens": rand_i8((rows, hidden), device, seed + 1),
+    r = streams(seed, 2)
+    return {"tokens": rand_i8((rows, hidden), device, r[0]),
             "counts": torch.from_numpy(counts).to(device=device, dtype=torch.int32),
-            "scales": rand_uniform((rows,), 0.005, 0.02, device, seed + 2)}
+            "scales": rand_uniform((rows,), 0.005, 0.02, device, r[1])}
 
 
 def make_finalize(device="cuda", tokens=16384, k=8, hidden=7168, seed=0):
-    g = _gen(device, seed + 3)
-    return {"epr": rand_normal((tokens * k, hidden), device, seed + 1, torch.bfloat16),
-            "esdr": torch.randperm(tokens * k, device=device, generator=g).to(torch.int32),
-            "scales": rand_uniform((tokens, k), 0.0, 0.25, device, seed + 2),
-            "skip1": rand_normal((tokens, hidden), device, seed + 4, torch.bfloat16)}
+    r = streams(seed, 4)
+    return {"epr": rand_normal((tokens * k, hidden), device, r[0], torch.bfloat16),
+            "esdr": torch.from_numpy(r[1].permutation(tokens * k).astype(np.int32)).to(device),
+            "scales": rand_uniform((tokens, k), 0.0, 0.25, device, r[2]),
+            "skip1": rand_normal((tokens, hidden), device, r[3], torch.bfloat16)}
 
 
 def make_dqsq(device="cuda", rows=131072, n2=4096, seed=0):
-    g = _gen(device, seed + 1)
-    return {"x": torch.randint(-(1 << 15), 1 << 15, (rows, n2), dtype=torch.int32, device=device, generator=g),
-            "weight_scale": rand_uniform((n2,), 1e-4, 1e-3, device, seed + 2),
-            "activation_scale": rand_uniform((rows,), 0.005, 0.02, device, seed + 3)}
+    r = streams(seed, 3)
+    return {"x": _fill((rows, n2), device, torch.int32,
+                       lambda n: r[0].integers(-(1 << 15), 1 << 15, size=n, dtype=np.int32)),
+            "weight_scale": rand_uniform((n2,), 1e-4, 1e-3, device, r[1]),
+            "activation_scale": rand_uniform((rows,), 0.005, 0.02, device, r[2])}

@@ -53,9 +53,12 @@ __device__ __forceinline__ float ld16(uint16_t h) { return BF16 ? bf16_to_f32(h)
 template <bool BF16>
 __device__ __forceinline__ uint16_t st16(float f) { return BF16 ? f32_to_bf16(f) : f32_to_f16(f); }
 
-// fp32 -> fp16 -> int8, both steps round-half-even; saturates, NaN -> 0.
+// fp32 -> fp16 -> int8, both steps round-half-even; saturates, NaN -> 0.  The empty asm keeps v a
+// rounded fp32 value: the compiler would otherwise fold a product feeding the fp16 conversion into
+// one mixed-precision fma (v_fma_mixlo_f16) that rounds once instead of twice.
 __device__ __forceinline__ int rint16(float v)
 {
+    asm volatile("" : "+v"(v));
     float h = __builtin_rintf((float)(_Float16)v);
     h = (h == h) ? h : 0.0f;  // NaN -> 0
     h = fminf(fmaxf(h, -128.0f), 127.0f);

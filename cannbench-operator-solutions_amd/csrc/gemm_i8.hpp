@@ -26,9 +26,7 @@
 
 namespace cb {
 
-// EPI_SWIGLU_Q: SwiGLU with the per-token requant fused (persistent prefill kernel; the fp32
-// activation stays on chip)
-enum { EPI_SWIGLU = 0, EPI_DEQUANT = 1, EPI_I32 = 2, EPI_SWIGLU_Q = 3 };
+enum { EPI_SWIGLU = 0, EPI_DEQUANT = 1, EPI_I32 = 2 };
 
 enum { BIAS_NONE = 0, BIAS_I32 = 1, BIAS_F16 = 2, BIAS_BF16 = 3, BIAS_F32 = 4 };
 
@@ -67,11 +65,13 @@ struct EpiArgs {
     float* act;
     u32* amax;
     int64_t H;
-    // fused requant (EPI_SWIGLU_Q)
+    // fused requant (the persistent prefill kernel, gmsq_prefill.hpp)
     u32* arrive;       // per row tile: column tiles that have published their row maxima
     u32* status;       // set to 1 if a row tile's exchange timed out
     int8_t* yq;        // int8 output [M, H]
     float* yq_scale;   // fp32 row scales [M]
+    u32* redo;         // per (row tile, column tile): the exchange wait timed out, the fix-up stores y
+    int32_t spin_limit;  // polls of the exchange wait before it gives up
 };
 
 struct GemmArgs {
@@ -319,11 +319,8 @@ __device__ __forceinline__ void skinny_row_epilogue(const GemmArgs& a, const int
 //   group c = l % 16 (16 consecutive weight columns); after the in-register 16x16 byte transpose
 //   the lane holds 16 B operands, one per column, and MFMA j yields column (16 c + j).
 // ============================================================================================
-#ifndef CB_SKINNY_OCC
-#define CB_SKINNY_OCC 2
-#endif
-template <int EPI, bool PREFETCH>
-__global__ __launch_bounds__(256, PREFETCH ? 2 : CB_SKINNY_OCC) void skinny_kernel(const GemmArgs a)
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void skinny_kernel(const GemmArgs a)
 {
     __shared__ int red[3][4][16][64];  // partial sums handed to the wave that owns them (48 KiB)
 
@@ -391,29 +388,11 @@ __global__ __launch_bounds__(256, PREFETCH ? 2 : CB_SKINNY_OCC) void skinny_kern
         };
         auto mma_chunk = [&](const uint4 (&R)[16], const v4i av) { skinny_mma_chunk(R, av, acc); };
 
-        if constexpr (PREFETCH) {
-            // the next chunk of this wave is always issued (chunks past K read zeros and fetch
-            // nothing), so the loop has no branch between the loads and the MFMAs that would make
-            // the compiler drain every outstanding load
+        for (int kc = wave; kc < nch; kc += 4) {
             uint4 R[16];
             v4i A;
-            load_chunk(wave, R, A);
-            for (int kc = wave; kc < nch; kc += 4) {
-                uint4 Rn[16];
-                v4i An;
-                load_chunk(kc + 4, Rn, An);
-                mma_chunk(R, A);
-#pragma unroll
-                for (int i = 0; i < 16; ++i) R[i] = Rn[i];
-                A = An;
-            }
-        } else {
-            for (int kc = wave; kc < nch; kc += 4) {
-                uint4 R[16];
-                v4i A;
-                load_chunk(kc, R, A);
-                mma_chunk(R, A);
-            }
+            load_chunk(kc, R, A);
+            mma_chunk(R, A);
         }
 
         // Cross-wave K reduction: wave w keeps accumulator row r == w and receives the other
@@ -444,21 +423,7 @@ __global__ __launch_bounds__(256, PREFETCH ? 2 : CB_SKINNY_OCC) void skinny_kern
     }
 }
 
-// ============================================================================================
-// tiled_kernel: prefill / dense.  BM x BN x 64 tiles, 4 waves in a WM x WN grid, 32x32x32 MFMA.
-// ============================================================================================
-constexpr int kNumXcd = 8;
-
-// Workgroups are dispatched round-robin over the 8 XCDs; renumber them so every XCD walks a
-// contiguous range of the tile order (tiles that share A rows / B columns share that XCD's L2).
-__device__ __forceinline__ int xcd_remap(int bid, int nblocks)
-{
-    const int xcd = bid % kNumXcd, local = bid / kNumXcd;
-    const int per = (nblocks + kNumXcd - 1) / kNumXcd;
-    const int tall = nblocks % kNumXcd == 0 ? kNumXcd : nblocks % kNumXcd;
-    return xcd < tall ? xcd * per + local : tall * per + (xcd - tall) * (per - 1) + local;
-}
-
+// Group of row tile mt in a GroupTable enumeration.
 __device__ __forceinline__ int group_of_tile(const GroupTable& gt, int mt)
 {
     int lo = 0, hi = gt.n_groups - 1;
@@ -468,260 +433,6 @@ __device__ __forceinline__ int group_of_tile(const GroupTable& gt, int mt)
         else hi = mid - 1;
     }
     return lo;
-}
-
-template <int EPI, int BM, int WM>
-struct TiledCfg {
-    static constexpr int BN = 256, BK = 64, PITCH = 80, WN = 4 / WM;
-    static constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
-    static constexpr int A_BYTES = BM * PITCH, B_BYTES = BN * PITCH;
-    static constexpr int STAGE = A_BYTES + B_BYTES;
-    static constexpr int NA = BM / 64;  // 16-byte A chunks per thread per stage
-    static_assert(FM >= 1 && FN >= 2 && (FN % 2) == 0, "tile shape");
-};
-
-template <int EPI, int BM, int WM>
-__global__ __launch_bounds__(256, 1) void tiled_kernel(const GemmArgs a)
-{
-    using C = TiledCfg<EPI, BM, WM>;
-    constexpr int BN = C::BN, BK = C::BK, PITCH = C::PITCH, TM = C::TM, TN = C::TN, FM = C::FM,
-                  FN = C::FN, NA = C::NA, WN = C::WN;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::STAGE];
-
-    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-    const int wm = wave / WN, wn = wave % WN;
-    const int64_t K = a.K, N = a.N;
-    const EpiArgs& e = a.epi;
-    const int64_t b = blockIdx.y;  // batch (dense QuantMatmul)
-
-    // ---- tile selection: XCD remap, then GROUP_M-swizzled (mt, nt) -------------------------
-    const int nblocks = gridDim.x;
-    const int pid = xcd_remap(blockIdx.x, nblocks);
-    constexpr int GROUP_M = 8;
-    const int T_m = a.gt.total_mtiles, T_n = a.ntiles;
-    const int per_group = GROUP_M * T_n;
-    const int gid = pid / per_group;
-    const int first_m = gid * GROUP_M;
-    const int gsz = (T_m - first_m) < GROUP_M ? (T_m - first_m) : GROUP_M;
-    const int mt = first_m + (pid % per_group) % gsz;
-    const int nt = (pid % per_group) / gsz;
-
-    const int g = group_of_tile(a.gt, mt);
-    const int rs = g ? a.gt.row_end[g - 1] : 0;
-    const int r1 = a.gt.row_end[g];
-    const int m0 = rs + (mt - a.gt.tile_start[g]) * BM;
-
-    const int8_t* xb = a.x + b * a.x_bstride;
-    const int8_t* wb = a.w + b * a.w_bstride + (int64_t)g * a.w_gstride;
-
-    // ---- global load assignment ------------------------------------------------------------
-    // A: chunk id = tid + 256 i -> tile row id / 4, k offset 16 (id % 4)
-    const int8_t* a_src[NA];
-#pragma unroll
-    for (int i = 0; i < NA; ++i) {
-        const int id = tid + 256 * i;
-        int row = m0 + (id >> 2);
-        row = row < r1 ? row : r1 - 1;
-        const int srow = src_row(a, row);  // an out-of-range gathered row reads row 0, scaled by 0
-        a_src[i] = xb + (int64_t)(srow >= 0 ? srow : 0) * K + (id & 3) * 16;
-    }
-    // B: thread -> 8 k rows (8 rg .. 8 rg + 7) x 8 tile columns (8 cg .. 8 cg + 7)
-    const int rg = tid & 7, cg = tid >> 3;
-    int64_t bcol;
-    bool bok;
-    if constexpr (EPI == EPI_SWIGLU) {
-        const int64_t H = e.H;
-        const int tc = 8 * cg;
-        const int64_t j = (int64_t)nt * (BN / 2) + (tc % (BN / 2));
-        bok = j < H;
-        bcol = tc < BN / 2 ? j : H + j;
-    } else {
-        bcol = (int64_t)nt * BN + 8 * cg;
-        bok = bcol < N;
-    }
-    const int8_t* b_src = wb + (bok ? bcol : 0) + (int64_t)(8 * rg) * N;
-
-    // wave-uniform skip of 32-row fragments that lie past the group end
-    bool fvalid[FM];
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm) fvalid[fm] = (m0 + wm * TM + fm * 32) < r1;
-
-    v16i acc[FM][FN];
-#pragma unroll
-    for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0;
-
-    const int nk = (int)((K + BK - 1) / BK);
-    uint4 ra[NA];
-    uint2 rb[8];
-
-    auto gload = [&](int kt) {
-        const int64_t k0 = (int64_t)kt * BK;
-#pragma unroll
-        for (int i = 0; i < NA; ++i) {
-            const int id = tid + 256 * i;
-            ra[i] = (k0 + (id & 3) * 16 < K) ? *reinterpret_cast<const uint4*>(a_src[i] + k0) : zero4();
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            rb[i] = (k0 + 8 * rg + i < K) ? *reinterpret_cast<const uint2*>(b_src + (k0 + i) * N)
-                                          : make_uint2(0u, 0u);
-    };
-    auto lstore = [&](int buf) {
-        uint8_t* As = smem + buf * C::STAGE;
-        uint8_t* Bs = As + C::A_BYTES;
-#pragma unroll
-        for (int i = 0; i < NA; ++i) {
-            const int id = tid + 256 * i;
-            *reinterpret_cast<uint4*>(As + (id >> 2) * PITCH + (id & 3) * 16) = ra[i];
-        }
-        // 8x8 byte transpose: rows 8 rg + i, columns 8 cg + s -> column-major k runs
-        u32 t[8][2];
-#pragma unroll
-        for (int hb = 0; hb < 2; ++hb) {      // row half (rows 4 hb .. 4 hb + 3)
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {  // column half
-                u32 o0, o1, o2, o3;
-                const u32 s0 = cb ? rb[4 * hb + 0].y : rb[4 * hb + 0].x;
-                const u32 s1 = cb ? rb[4 * hb + 1].y : rb[4 * hb + 1].x;
-                const u32 s2 = cb ? rb[4 * hb + 2].y : rb[4 * hb + 2].x;
-                const u32 s3 = cb ? rb[4 * hb + 3].y : rb[4 * hb + 3].x;
-                transpose4x4_b8(s0, s1, s2, s3, o0, o1, o2, o3);
-                t[4 * cb + 0][hb] = o0;
-                t[4 * cb + 1][hb] = o1;
-                t[4 * cb + 2][hb] = o2;
-                t[4 * cb + 3][hb] = o3;
-            }
-        }
-#pragma unroll
-        for (int s = 0; s < 8; ++s)
-            *reinterpret_cast<uint2*>(Bs + (8 * cg + s) * PITCH + 8 * rg) = make_uint2(t[s][0], t[s][1]);
-    };
-
-    auto tcol = [&](int fn) -> int {
-        if constexpr (EPI == EPI_SWIGLU)
-            return fn < FN / 2 ? wn * (TN / 2) + fn * 32 : BN / 2 + wn * (TN / 2) + (fn - FN / 2) * 32;
-        else
-            return wn * TN + fn * 32;
-    };
-
-    gload(0);
-    lstore(0);
-    __syncthreads();
-
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) gload(kt + 1);
-        const uint8_t* As = smem + cur * C::STAGE;
-        const uint8_t* Bs = As + C::A_BYTES;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const int ko = ks * 32 + (lane >> 5) * 16;
-            v4i af[FM], bf[FN];
-#pragma unroll
-            for (int fm = 0; fm < FM; ++fm)
-                af[fm] = *reinterpret_cast<const v4i*>(As + (wm * TM + fm * 32 + (lane & 31)) * PITCH + ko);
-#pragma unroll
-            for (int fn = 0; fn < FN; ++fn)
-                bf[fn] = *reinterpret_cast<const v4i*>(Bs + (tcol(fn) + (lane & 31)) * PITCH + ko);
-#pragma unroll
-            for (int fm = 0; fm < FM; ++fm) {
-                if (fvalid[fm]) {
-#pragma unroll
-                    for (int fn = 0; fn < FN; ++fn)
-                        acc[fm][fn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[fm], bf[fn], acc[fm][fn], 0, 0, 0);
-                }
-            }
-        }
-        if (kt + 1 < nk) lstore(cur ^ 1);
-        __syncthreads();
-    }
-
-    // ---- epilogue.  32x32 C layout: lane l holds column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4
-    const int lr = (lane >> 5) * 4;
-    if constexpr (EPI == EPI_SWIGLU) {
-        const int64_t H = e.H;
-        float wsg[FN / 2], wsu[FN / 2];
-        int64_t jc[FN / 2];
-        bool jok[FN / 2];
-#pragma unroll
-        for (int fn = 0; fn < FN / 2; ++fn) {
-            jc[fn] = (int64_t)nt * (BN / 2) + wn * (TN / 2) + fn * 32 + (lane & 31);
-            jok[fn] = jc[fn] < H;
-            wsg[fn] = jok[fn] ? e.w_scale[(int64_t)g * N + jc[fn]] : 0.0f;
-            wsu[fn] = jok[fn] ? e.w_scale[(int64_t)g * N + H + jc[fn]] : 0.0f;
-        }
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm) {
-            if (!fvalid[fm]) continue;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * TM + fm * 32 + (r >> 2) * 8 + lr + (r & 3);
-                const bool rowok = row < r1;
-                const float xs = rowok ? src_x_scale(a, row) : 0.0f;
-                float m = 0.0f;
-#pragma unroll
-                for (int fn = 0; fn < FN / 2; ++fn) {
-                    if (rowok && jok[fn]) {
-                        const float v = swiglu((float)acc[fm][fn][r], (float)acc[fm][fn + FN / 2][r], xs,
-                                               wsg[fn], wsu[fn]);
-                        e.act[(int64_t)row * H + jc[fn]] = v;
-                        m = fmaxf(m, fabsf(v));
-                    }
-                }
-#pragma unroll
-                for (int o = 1; o < 32; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-                if ((lane & 31) == 0 && rowok) atomicMax(e.amax + row, __float_as_uint(m));
-            }
-        }
-    } else if constexpr (EPI == EPI_I32) {
-        int32_t* ob = (int32_t*)e.out + b * e.out_bstride;
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm) {
-            if (!fvalid[fm]) continue;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * TM + fm * 32 + (r >> 2) * 8 + lr + (r & 3);
-                if (row >= r1) continue;
-#pragma unroll
-                for (int fn = 0; fn < FN; ++fn) {
-                    const int64_t col = (int64_t)nt * BN + wn * TN + fn * 32 + (lane & 31);
-                    if (col < N) ob[(int64_t)row * N + col] = acc[fm][fn][r];
-                }
-            }
-        }
-    } else {
-        ColDeq cd[FN];
-        int64_t cc[FN];
-        bool cok[FN];
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn) {
-            cc[fn] = (int64_t)nt * BN + wn * TN + fn * 32 + (lane & 31);
-            cok[fn] = cc[fn] < N;
-            cd[fn] = col_deq(e, g, b, cok[fn] ? cc[fn] : 0);
-        }
-        uint16_t* ob = (uint16_t*)e.out + b * e.out_bstride;
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm) {
-            if (!fvalid[fm]) continue;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * TM + fm * 32 + (r >> 2) * 8 + lr + (r & 3);
-                if (row >= r1) continue;
-                const float pt = e.has_pt ? e.pertoken[row] : 1.0f;
-#pragma unroll
-                for (int fn = 0; fn < FN; ++fn) {
-                    if (cok[fn]) {
-                        const float v = apply_deq(e, cd[fn], acc[fm][fn][r], pt);
-                        ob[(int64_t)row * N + cc[fn]] = e.out_bf16 ? f32_to_bf16(v) : f32_to_f16(v);
-                    }
-                }
-            }
-        }
-    }
 }
 
 // ============================================================================================

@@ -26,12 +26,6 @@ typedef int v2i __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 #define CB_LDS __attribute__((address_space(3)))
 
-// Polls of a row tile's arrival counter before the fused requant gives up (each poll sleeps about
-// 512 cycles plus an atomic round trip: about 2 s in total, against microseconds normally; long
-// enough for kernels on other streams that hold CUs to drain before the grid is all resident).
-// A timeout sets the workspace status word (cb_grouped_matmul_swiglu_quant_status).
-constexpr int kExchangeSpinLimit = 1 << 20;
-
 // The LDS DMA and the stage barrier are written as inline asm on purpose: when the compiler sees
 // buffer_load ... lds it must assume every later LDS read may alias the DMA target and waits for
 // vmcnt(0), and a __syncthreads() fence also drains vmcnt - either would serialise the stage
@@ -41,10 +35,7 @@ constexpr int kExchangeSpinLimit = 1 << 20;
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t lds_addr)
 {
-#ifndef CB_DMA_MOD
-#define CB_DMA_MOD ""
-#endif
-    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen" CB_DMA_MOD " lds" ::"v"(voff), "s"(rsrc),
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc),
                  "s"(lds_addr)
                  : "memory", "m0");
 }
@@ -53,15 +44,6 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff
 // Workgroup barrier after the main loop: every wave's LDS reads and DMAs (including the stages
 // issued past the end of K) are drained, so the stage buffers can be reused for epilogue staging.
 __device__ __forceinline__ void epi_barrier() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-#ifdef CB_PROFILE
-__device__ unsigned long long cb_prof[8];
-#define CB_PROF_T(v) uint64_t v = __builtin_amdgcn_s_memtime()
-#define CB_PROF_ADD(slot, t0) do { uint64_t _t = __builtin_amdgcn_s_memtime(); prof_acc[slot] += _t - (t0); } while (0)
-#else
-#define CB_PROF_T(v)
-#define CB_PROF_ADD(slot, t0)
-#endif
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt_barrier()
@@ -113,17 +95,22 @@ struct TileDma {
     __device__ __forceinline__ void init(const GemmArgs& a, const int mt, const int nt, const int64_t b, const int wave,
                                          const int lane)
     {
+        const int g = group_of_tile(a.gt, mt);
+        const int m0 = (g ? a.gt.row_end[g - 1] : 0) + (mt - a.gt.tile_start[g]) * C::BM;
+        init_at(a, g, m0, a.gt.row_end[g] - m0, nt, b, wave, lane);
+    }
+
+    // The plan of the tile of group g whose rows start at m0 (vrows of them valid).
+    __device__ __forceinline__ void init_at(const GemmArgs& a, const int g, const int m0, const int vrows, const int nt,
+                                            const int64_t b, const int wave, const int lane)
+    {
         constexpr int BM = C::BM, BN = C::BN, NW = C::NW, ACH = C::ACH;
         const int64_t K = a.K, N = a.N;
-        const int g = group_of_tile(a.gt, mt);
-        const int rs = g ? a.gt.row_end[g - 1] : 0;
-        const int m0 = rs + (mt - a.gt.tile_start[g]) * BM;
-        const int vrows = a.gt.row_end[g] - m0;
         // A = rows [m0, r1) of x (with a row index: all of x, rows gathered through the per-lane
         // offsets), B = this group's weight [K, N]
         const bool gather = a.row_index != nullptr;
         ares = gather ? make_rsrc(a.x, (uint32_t)(a.x_rows * K))
-                      : make_rsrc(a.x + b * a.x_bstride + (int64_t)m0 * K, (uint32_t)((int64_t)vrows * K));
+                      : make_rsrc(a.x + b * a.x_bstride + (int64_t)m0 * K, (uint32_t)((int64_t)(vrows < BM ? vrows : BM) * K));
         bres = make_rsrc(a.w + b * a.w_bstride + (int64_t)g * a.w_gstride, (uint32_t)(K * N));
         n = (uint32_t)N;
         nk = (int)((K + C::BK - 1) / C::BK);
@@ -170,6 +157,23 @@ struct TileDma {
         nk = 0;
     }
 
+    // DMA chunk I of stage kt (I < A_ISSUE: activation chunk I, else weight chunk I - A_ISSUE) into
+    // ring slot `slot`; the same addressing as issue_at.
+    template <int I>
+    __device__ __forceinline__ void issue_one(const int kt, const int slot, const uint32_t lds_base, const int wave) const
+    {
+        constexpr int NW = C::NW;
+        const uint32_t sa = lds_base + (uint32_t)(slot * C::STAGE);
+        if constexpr (I < C::A_ISSUE) {
+            dma16(ares, kt < nk ? a_off[I] + (uint32_t)(kt * C::BK) : 0x80000000u,
+                  __builtin_amdgcn_readfirstlane(sa + (uint32_t)((I * NW + wave) * 1024)));
+        } else {
+            constexpr int J = I - C::A_ISSUE;
+            dma16(bres, b_off[J] + (uint32_t)(kt * C::BK) * n,
+                  __builtin_amdgcn_readfirstlane(sa + C::A_BYTES + (uint32_t)((J * NW + wave) * 1024)));
+        }
+    }
+
     // DMAs of stage kt into ring slot kt % STAGES.
     __device__ __forceinline__ void issue(const int kt, const uint32_t lds_base, const int wave) const
     {
@@ -199,7 +203,7 @@ struct TileDma {
 };
 
 template <int EPI, int WM, int WN, int STAGES, int BKT>
-using TileDmaOf = TileDma<LdsCfg<WM, WN, STAGES, BKT>, EPI == EPI_SWIGLU || EPI == EPI_SWIGLU_Q>;
+using TileDmaOf = TileDma<LdsCfg<WM, WN, STAGES, BKT>, EPI == EPI_SWIGLU>;
 
 // One 256 x 256 output tile (row tile mt, column tile nt, batch b).  Called once per workgroup by
 // lds_gemm_kernel and in a loop by the persistent kernels.
@@ -210,13 +214,13 @@ using TileDmaOf = TileDma<LdsCfg<WM, WN, STAGES, BKT>, EPI == EPI_SWIGLU || EPI 
 // the plan `nxt`.  The epilogue then writes from registers and leaves the LDS ring to those DMAs.
 template <int EPI, int WM, int WN, int STAGES, int BKT, bool CONT = false>
 __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, const int nt, const int64_t b,
-                                              uint8_t* smem, const int arr_idx = 0, const u32 arr_target = 0,
+                                              uint8_t* smem,
                                               const TileDmaOf<EPI, WM, WN, STAGES, BKT>* cur = nullptr,
                                               const TileDmaOf<EPI, WM, WN, STAGES, BKT>* nxt = nullptr,
                                               const int sbase = 0, const int xs_slot = 0)
 {
     using C = LdsCfg<WM, WN, STAGES, BKT>;
-    constexpr bool SW = EPI == EPI_SWIGLU || EPI == EPI_SWIGLU_Q;
+    constexpr bool SW = EPI == EPI_SWIGLU;
     constexpr int KS = C::KS, ACH = C::ACH;
     constexpr int BM = C::BM, BN = C::BN, BK = C::BK, TN = C::TN, FM = C::FM,
                   FN = C::FN;
@@ -327,7 +331,7 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
     } else if constexpr (EPI == EPI_DEQUANT) {
         const int lr0 = tid % BM;
         const __amdgpu_buffer_rsrc_t pres =
-            e.has_pt ? make_rsrc(e.pertoken + m0, (uint32_t)(vrows * 4)) : make_rsrc(a.x, 0u);
+            e.has_pt ? make_rsrc(e.pertoken + m0, (uint32_t)((vrows < BM ? vrows : BM) * 4)) : make_rsrc(a.x, 0u);
         const float v = __builtin_bit_cast(
             float, __builtin_amdgcn_raw_buffer_load_b32(pres, (uint32_t)((lr0 < vrows ? lr0 : vrows - 1) * 4), 0, 0));
         xs_pre = e.has_pt ? v : 1.0f;
@@ -366,7 +370,6 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
         auto load = [&](int kt, int ks, v4i (&af)[NVA], v4i (&bf)[FN]) {
             if constexpr (NV > 0) {
                 const CB_LDS uint8_t* base = (const CB_LDS uint8_t*)smem + slot_of(kt) * C::STAGE;
-#ifndef CB_ABLATE_NO_LDSREAD
 #pragma unroll
                 for (int fm = 0; fm < NV; ++fm) af[fm] = *(const CB_LDS v4i*)(base + a_rd[fm][ks]);
 #pragma unroll
@@ -375,33 +378,19 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
                     const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((CB_LDS v2i*)(base + b_rd_at(fn, ks, 1)));
                     bf[fn] = v4i{lo[0], lo[1], hi[0], hi[1]};
                 }
-#else
-#pragma unroll
-                for (int fm = 0; fm < NV; ++fm) af[fm] = v4i{kt, ks, fm, lane};
-#pragma unroll
-                for (int fn = 0; fn < FN; ++fn) bf[fn] = v4i{fn, kt, lane, ks};
-#endif
             }
         };
         auto mma = [&](const v4i (&af)[NVA], const v4i (&bf)[FN]) {
             if constexpr (NV > 0) {
-#ifndef CB_ABLATE_NO_MFMA
 #pragma unroll
                 for (int fm = 0; fm < NV; ++fm)
 #pragma unroll
                     for (int fn = 0; fn < FN; ++fn)
                         acc[fm][fn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[fm], bf[fn], acc[fm][fn], 0, 0, 0);
-#else
-#pragma unroll
-                for (int fm = 0; fm < NV; ++fm)
-#pragma unroll
-                    for (int fn = 0; fn < FN; ++fn) acc[fm][fn][0] ^= af[fm][0] ^ bf[fn][1];
-#endif
             }
         };
         // one DS read after each MFMA while reads remain, then the remaining MFMAs
         auto interleave = [&]() {
-#if !defined(CB_NO_SCHED_HINTS) && !defined(CB_ABLATE_NO_MFMA) && !defined(CB_ABLATE_NO_LDSREAD)
             if constexpr (NV > 0) {
                 constexpr int NMFMA = NV * FN, NREAD = NV + 2 * FN;
                 constexpr int PAIRS = NMFMA < NREAD ? NMFMA : NREAD;
@@ -413,16 +402,8 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
                 if constexpr (NMFMA > PAIRS) __builtin_amdgcn_sched_group_barrier(0x0008, NMFMA - PAIRS, 0);
                 if constexpr (NREAD > PAIRS) __builtin_amdgcn_sched_group_barrier(0x0100, NREAD - PAIRS, 0);
             }
-#endif
         };
         constexpr int LATER = STAGES - 2;  // stages after the awaited one that stay in flight
-#ifdef CB_PROFILE
-        uint64_t prof_acc[4] = {0, 0, 0, 0};
-        CB_PROF_T(tstart);
-#ifdef CB_PROFILE
-        const uint64_t rstart = __builtin_amdgcn_s_memrealtime();
-#endif
-#endif
         wait_vmcnt_barrier<(STAGES - 1) * C::ISSUE>();
         load(0, 0, a0, b0);
         for (int kt = 0; kt < nk; ++kt) {
@@ -434,14 +415,8 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
                 mma(a0, b0);
                 interleave();
                 if (ks + 2 == KS) {
-                    CB_PROF_T(tw);
                     wait_vmcnt_barrier<LATER * C::ISSUE>();
-                    CB_PROF_ADD(0, tw);
-                    CB_PROF_T(td);
-#ifndef CB_ABLATE_NO_DMA
                     issue_stage(kt + STAGES);
-#endif
-                    CB_PROF_ADD(1, td);
                     load(kt + 1, 0, a0, b0);
                 } else {
                     load(kt, ks + 2, a0, b0);
@@ -450,21 +425,6 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
                 interleave();
             }
         }
-#ifdef CB_PROFILE
-        CB_PROF_ADD(2, tstart);
-        if (lane == 0) {
-            atomicAdd(&cb_prof[0], prof_acc[0]);
-            atomicAdd(&cb_prof[1], prof_acc[1]);
-            atomicAdd(&cb_prof[2], prof_acc[2]);
-            atomicAdd(&cb_prof[3], 1ull);
-            // the shader clock follows from memtime (core clock) over memrealtime (100 MHz)
-            atomicAdd(&cb_prof[4], __builtin_amdgcn_s_memrealtime() - rstart);
-            if (vrows < BM) {
-                atomicAdd(&cb_prof[5], prof_acc[2]);
-                atomicAdd(&cb_prof[6], 1ull);
-            }
-        }
-#endif
     };
     static_assert(FM <= 4, "loop variants below cover up to 4 fragments");
     if (nvf >= FM) kloop(std::integral_constant<int, FM>());
@@ -477,19 +437,6 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) fvalid[fm] = fm < nvf;
 
-#ifdef CB_ABLATE_NO_EPI
-    {
-        int sum = 0;
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-            for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) sum += acc[fm][fn][r];
-        asm volatile("" ::"v"(sum));  // keeps the accumulators live without a store
-        return;
-    }
-#endif
     // ---- epilogue.  32x32 C layout: lane l holds column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4
     const int lr = (lane >> 5) * 4;
     if constexpr (CONT) {
@@ -501,7 +448,7 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
         const int64_t col0 = (int64_t)nt * BN + wn * TN + (lane & 31);
         if constexpr (EPI == EPI_I32) {
             const __amdgpu_buffer_rsrc_t ores =
-                make_rsrc((int32_t*)e.out + b * e.out_bstride + (int64_t)m0 * N, (uint32_t)(vrows * N * 4));
+                make_rsrc((int32_t*)e.out + b * e.out_bstride + (int64_t)m0 * N, (uint32_t)((vrows < BM ? vrows : BM) * N * 4));
             uint32_t coff[FN];
 #pragma unroll
             for (int fn = 0; fn < FN; ++fn) coff[fn] = col0 + 32 * fn < N ? (uint32_t)(col0 + 32 * fn) * 4u : 0x80000000u;
@@ -521,7 +468,7 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
             // adjacent columns of one row as one dword: the even lane row r, columns (c, c + 1),
             // the odd lane row r + 1, columns (c - 1, c).
             const __amdgpu_buffer_rsrc_t ores =
-                make_rsrc((uint16_t*)e.out + b * e.out_bstride + (int64_t)m0 * N, (uint32_t)(vrows * N * 2));
+                make_rsrc((uint16_t*)e.out + b * e.out_bstride + (int64_t)m0 * N, (uint32_t)((vrows < BM ? vrows : BM) * N * 2));
             const bool odd = lane & 1;
             ColDeq cd[FN];
             uint32_t coff[FN];
@@ -612,90 +559,20 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
         const int64_t j0 = (int64_t)nt * (BN / 2) + part * CPT;
         const CB_LDS v4f* src = (const CB_LDS v4f*)(st + lrow * C::EPI_PITCH + part * CPT * 4);
         float m = 0.0f;
-        if constexpr (EPI == EPI_SWIGLU) {
-            if (row < r1) {
-                v4f* dst = reinterpret_cast<v4f*>(e.act + (int64_t)row * H + j0);
-#pragma unroll
-                for (int i = 0; i < CPT / 4; ++i) {
-                    if (j0 + 4 * i < H) {
-                        const v4f v = src[i];
-                        dst[i] = v;
-                        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
-                    }
-                }
-            }
-#pragma unroll
-            for (int o = 1; o < TPR; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-            if (part == 0 && row < r1) atomicMax(e.amax + row, __float_as_uint(m));
-        } else {
-            // Fused requant.  The thread keeps its 64 act values in registers; the row maxima of the
-            // ntiles column tiles of this row tile (all resident at once in the persistent grid) are
-            // combined with device-scope atomics, and each tile quantises its own slice once every
-            // workgroup of its exchange group (arr_target of them, counted at arrive[arr_idx]) has
-            // published.  The fp32 activation never leaves the CU.
-            v4f v[CPT / 4];
+        if (row < r1) {
+            v4f* dst = reinterpret_cast<v4f*>(e.act + (int64_t)row * H + j0);
 #pragma unroll
             for (int i = 0; i < CPT / 4; ++i) {
-                v[i] = src[i];
-                if (row < r1 && j0 + 4 * i < H)
-                    m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i][0]), fabsf(v[i][1])), fmaxf(fabsf(v[i][2]), fabsf(v[i][3]))));
-            }
-#pragma unroll
-            for (int o = 1; o < TPR; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-            // Every shared word of the exchange (row maxima, arrival counts) is touched only by
-            // agent-scope atomics, which are coherent across the XCDs without flushing or
-            // invalidating L2 (a __threadfence() here would invalidate the GEMM's cached slabs).
-            // Ordering: each maximum has completed (vmcnt 0) before the barrier, and the arrival
-            // count is bumped after it.
-            if (part == 0 && row < r1)
-                __hip_atomic_fetch_max(e.amax + row, __float_as_uint(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();
-            if (tid == 0) {
-                __hip_atomic_fetch_add(e.arrive + arr_idx, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                // bounded wait: every wave reaches the end even if a column tile never arrives (the
-                // status word then reports the failure and the tile quantises with what it has)
-                int spins = 0;
-#ifdef CB_PROFILE
-                const uint64_t tx0 = __builtin_amdgcn_s_memtime();
-#endif
-                while (__hip_atomic_load(e.arrive + arr_idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < arr_target) {
-                    __builtin_amdgcn_s_sleep(8);
-                    if (++spins > kExchangeSpinLimit) {
-                        __hip_atomic_fetch_or(e.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        break;
-                    }
-                }
-#ifdef CB_PROFILE
-                atomicAdd(&cb_prof[7], __builtin_amdgcn_s_memtime() - tx0);
-#endif
-            }
-            __syncthreads();
-            if (row < r1) {
-                // the final row maximum (an agent-scope atomic load sees every tile's update)
-                float am = __uint_as_float(
-                    __hip_atomic_load(e.amax + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-                if (!(am > kFltMin)) am = kFltMin;
-                const float inv = 127.0f / am;
-                if (nt == 0 && part == 0) e.yq_scale[row] = am * kInv127;
-                int8_t* dst = e.yq + (int64_t)row * H + j0;
-#pragma unroll
-                for (int c = 0; c < CPT / 16; ++c) {
-                    if (j0 + 16 * c < H) {
-                        v4i w;
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            const v4f t = v[4 * c + q];
-                            // clamp then narrow == saturating rint16; an all-zero row gives 0 * inf =
-                            // NaN, which rint16 maps to 0 (the standalone requant's rule)
-                            w[q] = (int)pack4_i8(rint16(t[0] * inv), rint16(t[1] * inv), rint16(t[2] * inv),
-                                                 rint16(t[3] * inv));
-                        }
-                        *reinterpret_cast<v4i*>(dst + 16 * c) = w;
-                    }
+                if (j0 + 4 * i < H) {
+                    const v4f v = src[i];
+                    dst[i] = v;
+                    m = fmaxf(m, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
                 }
             }
         }
+#pragma unroll
+        for (int o = 1; o < TPR; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if (part == 0 && row < r1) atomicMax(e.amax + row, __float_as_uint(m));
     } else if constexpr (EPI == EPI_I32) {
         int32_t* ob = (int32_t*)e.out + b * e.out_bstride;
 #pragma unroll
@@ -780,12 +657,9 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
 
 // Tile pid of the non-persistent launch order: GROUP_M row tiles x all column tiles per group of
 // pids, so the workgroups resident together share GROUP_M activation slabs and their weights.
-#ifndef CB_GROUP_M
-#define CB_GROUP_M 4
-#endif
 __device__ __forceinline__ void tile_of_pid(const GemmArgs& a, const int pid, int& mt, int& nt)
 {
-    constexpr int GROUP_M = CB_GROUP_M;
+    constexpr int GROUP_M = 4;
     const int T_m = a.gt.total_mtiles, T_n = a.ntiles;
     const int per_group = GROUP_M * T_n;
     const int gid = pid / per_group;
@@ -803,11 +677,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_kernel(const GemmArg
     // ---- tile selection (GROUP_M swizzle) ---------------------------------------------------
     // Measured on the prefill and dense shapes: the plain dispatch order (workgroups round-robin
     // over the XCDs) is as good as or better than an XCD-contiguous remap of the tile order.
-#ifdef CB_XCD_REMAP
-    const int pid = xcd_remap(blockIdx.x, gridDim.x);
-#else
     const int pid = blockIdx.x;
-#endif
     int mt, nt;
     tile_of_pid(a, pid, mt, nt);
     lds_gemm_tile<EPI, WM, WN, STAGES, BKT>(a, mt, nt, blockIdx.y, smem);
@@ -843,7 +713,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_persistent_kernel(co
         } else {
             nxt.set_dead(a);
         }
-        lds_gemm_tile<EPI, WM, WN, STAGES, BKT, true>(a, mt, nt, 0, smem, 0, 0, &cur, &nxt, sbase, xs_slot);
+        lds_gemm_tile<EPI, WM, WN, STAGES, BKT, true>(a, mt, nt, 0, smem, &cur, &nxt, sbase, xs_slot);
         if (pn >= total) break;
         xs_slot ^= 1;
         sbase = (sbase + cur.nk) % STAGES;
@@ -854,50 +724,6 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_persistent_kernel(co
     }
     // the dead stages issued by the last tile fetch nothing; drain them before the wave ends
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-}
-
-// Persistent GroupedMatmulSwigluQuant with the requant fused.  gridDim.x workgroups, at most one per
-// CU, all resident together.  A slot is RT consecutive row tiles x ntiles column tiles; its
-// workgroups compute round r's row tiles (slot + slots * r) * RT .. + RT - 1 and meet once per round
-// at the row-max exchange, which keeps the RT row tiles of the slot in step through K.  With 16
-// column tiles on 256 CUs (RT = 4, 4 slots) workgroup b (dispatched to XCD b % 8) gets slot
-// (b % 8) / 2: each XCD holds 4 row tiles x the same 8 column tiles, the GROUP_M = 4 footprint of
-// the non-persistent kernel, and the 8 workgroups sharing an activation slab sit on one XCD.
-template <int WM, int WN, int STAGES, int BKT>
-__global__ __launch_bounds__(64 * WM * WN, 1) void lds_gemm_swiglu_q_kernel(const GemmArgs a)
-{
-    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-    const int ntl = a.ntiles;
-    int slot, rt, nt, slots, RT;
-    if (ntl == 16 && gridDim.x == 256) {
-        // measured: this round-robin-aware assignment beats a contiguous one (blocks 64 s .. 64 s + 63
-        // per slot) by 20%, which confirms the round-robin dispatch over the XCDs
-        const int x = blockIdx.x & 7, j = blockIdx.x >> 3;
-        slot = x >> 1;
-        rt = j >> 3;
-        nt = (x & 1) * 8 + (j & 7);
-        slots = 4;
-        RT = 4;
-    } else {
-        slot = blockIdx.x / ntl;
-        rt = 0;
-        nt = blockIdx.x % ntl;
-        slots = (int)gridDim.x / ntl;
-        RT = 1;
-    }
-    const u32 target = (u32)(RT * ntl);
-    for (int q = slot; q * RT < a.gt.total_mtiles; q += slots) {
-        const int mt = q * RT + rt;
-        if (mt < a.gt.total_mtiles) {
-            lds_gemm_tile<EPI_SWIGLU_Q, WM, WN, STAGES, BKT>(a, mt, nt, 0, smem, q, target);
-        } else {
-            // past the last row tile in the final round: still take part in the exchange so the
-            // slot's other row tiles see every arrival
-            if (threadIdx.x == 0)
-                __hip_atomic_fetch_add(a.epi.arrive + q, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __syncthreads();  // the next tile's DMAs overwrite the LDS this epilogue just read
-    }
 }
 
 }  // namespace cb

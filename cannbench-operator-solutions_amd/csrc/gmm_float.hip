@@ -444,13 +444,9 @@ __global__ __launch_bounds__(256) void gmm_generic_kernel(const GmmFArgs a)
     }
 }
 
-// CANNBENCH_AMD_GMM_TILE=128 selects the 128 x 128 register-staged kernel for every fp16/bf16 shape
-// (it is otherwise taken only where a 256-row block of x or y passes 2 GiB); read on every call.
-static bool gmm_lds_enabled()
-{
-    const char* s = std::getenv("CANNBENCH_AMD_GMM_TILE");
-    return !(s && std::atoi(s) == 128);
-}
+// A test override of 128 selects the 128 x 128 register-staged kernel for every fp16/bf16 shape (it
+// is otherwise taken only where a 256-row block of x or y passes 2 GiB).
+static bool gmm_lds_enabled() { return g_overrides.gmm_tile != 128; }
 
 // Raise a kernel's dynamic LDS limit once per (kernel, device).
 static void set_dynamic_lds_once(const void* kern, int bytes)

@@ -78,6 +78,15 @@ inline int check_launch()
     return hipGetLastError() == hipSuccess ? CB_OK : CB_ERR_LAUNCH;
 }
 
+// Test hooks (set by cb_set_test_overrides, per thread, until changed): a forced grid for the
+// persistent GEMM kernels (0: the CU count; < 0: persistent launch off), a poll limit for the
+// GroupedMatmulSwigluQuant exchange wait (0: the default), and the GroupedMatmul tile (128 forces
+// the 128 x 128 kernel; 0: automatic).
+struct TestOverrides {
+    int persistent_grid = 0, exchange_spin_limit = 0, gmm_tile = 0;
+};
+extern thread_local TestOverrides g_overrides;
+
 // Optional per-thread instrumentation: events recorded around the next main kernel launch of an
 // operator (set by cb_set_kernel_timing, consumed and cleared by that launch).
 struct KernelTiming {

@@ -10,7 +10,7 @@
 #include <set>
 #include <utility>
 
-#include "gemm_lds.hpp"
+#include "gmsq_prefill.hpp"
 
 namespace cb {
 
@@ -65,21 +65,24 @@ static void fill_u32(u32* p, int64_t n, u32 v, hipStream_t st)
 static inline int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
 // Workspace layout of GroupedMatmulSwigluQuant: u32 row abs-max [M], u32 arrival counters (one per
-// 256-row tile; at most M / 256 + E tiles), a u32 status word, then the fp32 activation [M, H] that
-// only the non-persistent paths (decode-shaped groups, unaligned shapes) write.
+// exchange round; at most M / 256 + E + 2 rounds), a u32 status word, u32 fix-up marks (one per
+// 256-row x 128-column tile), then the fp32 activation [M, H] that only the non-persistent paths
+// (decode-shaped groups, unaligned shapes) write.
 struct GmsqWorkspace {
-    int64_t amax_off, arrive_off, status_off, act_off, total, n_arrive;
+    int64_t amax_off, arrive_off, status_off, redo_off, act_off, total, n_arrive, n_redo;
 };
 
 static GmsqWorkspace gmsq_workspace(int64_t M, int64_t N, int64_t E)
 {
     GmsqWorkspace w;
     const int64_t H = N / 2;
-    w.n_arrive = M / 256 + E + 1;
+    w.n_arrive = M / 256 + E + 2;
+    w.n_redo = (M / 256 + E) * ((H + 127) / 128);
     w.amax_off = 0;
     w.arrive_off = round_up(M * 4, 256);
     w.status_off = w.arrive_off + round_up(w.n_arrive * 4, 256);
-    w.act_off = w.status_off + 256;
+    w.redo_off = w.status_off + 256;
+    w.act_off = w.redo_off + round_up(w.n_redo * 4, 256);
     w.total = w.act_off + round_up(M * H * 4, 256);
     return w;
 }
@@ -99,15 +102,20 @@ static int device_cus()
     return cus[dev];
 }
 
-// Workgroups of the persistent dequant / int32 GEMM: one per CU.  CANNBENCH_AMD_PERSISTENT_GRID
-// overrides it (a small grid makes every workgroup walk many tiles: the parity tests use it);
-// a value <= 0 turns the persistent launch off.
+thread_local TestOverrides g_overrides;
+
+// Workgroups of the persistent dequant / int32 GEMM: one per CU, unless a test forces a small grid
+// (every workgroup then walks many tiles) or turns the persistent launch off.
 static int persistent_grid()
 {
-    const char* s = std::getenv("CANNBENCH_AMD_PERSISTENT_GRID");
-    if (s && *s) return std::atoi(s);
+    if (g_overrides.persistent_grid != 0) return g_overrides.persistent_grid;
     return device_cus();
 }
+
+// Polls of the GroupedMatmulSwigluQuant exchange wait before a tile gives up (each poll sleeps about
+// 512 cycles plus an atomic round trip: about 2 s in total, against microseconds normally).  A tile
+// that gives up is recomputed by the fix-up launch, so the limit bounds the wait, not correctness.
+static constexpr int kExchangeSpins = 1 << 20;
 
 // Raise a kernel's dynamic LDS limit once per (kernel, device): the attribute belongs to the
 // kernel as loaded on the current device, so a process driving several GPUs sets it on each.
@@ -123,36 +131,9 @@ static void allow_dynamic_lds(const void* kern, int bytes)
 }
 
 static constexpr int kSkinnyMaxRows = 32;  // groups up to this many rows take the skinny core
-static constexpr int kTiledBM = 128;
-#ifndef CB_SKINNY_PREFETCH
-#define CB_SKINNY_PREFETCH 0
-#endif
-static constexpr bool kSkinnyPrefetch = CB_SKINNY_PREFETCH;
-#ifndef CB_LDS_CORE
-#define CB_LDS_CORE 1
-#endif
-#ifndef CB_LDS_WM
-#define CB_LDS_WM 4
-#endif
-#ifndef CB_LDS_WN
-#define CB_LDS_WN 2
-#endif
-#ifndef CB_LDS_STAGES
-#define CB_LDS_STAGES 2
-#endif
-#ifndef CB_LDS_BK
-#define CB_LDS_BK 128
-#endif
-#ifndef CB_FUSED_REQUANT
-#define CB_FUSED_REQUANT 1
-#endif
-#ifndef CB_PERSISTENT_GEMM
-#define CB_PERSISTENT_GEMM 1
-#endif
-static constexpr bool kUseLdsCore = CB_LDS_CORE;
-static constexpr bool kPersistentGemm = CB_PERSISTENT_GEMM;
-static constexpr bool kFusedRequant = CB_FUSED_REQUANT;
-static constexpr int kLdsWM = CB_LDS_WM, kLdsWN = CB_LDS_WN, kLdsStages = CB_LDS_STAGES, kLdsBK = CB_LDS_BK;
+// The LDS core for prefill / dense groups: 256 x 256 tiles, 8 waves of 64 x 128, a 2-stage ring of
+// 128-deep stages.
+static constexpr int kLdsWM = 4, kLdsWN = 2, kLdsStages = 2, kLdsBK = 128;
 
 thread_local KernelTiming g_timing;
 
@@ -161,7 +142,8 @@ static void launch_gemm(GemmArgs& a, const int64_t* gl, int64_t E, int64_t batch
 {
     TimedLaunch timed(st);
     const int64_t Ncols = (EPI == EPI_SWIGLU) ? a.epi.H : a.N;  // output columns
-    build_group_table(a.gt, gl, E, kTiledBM);
+    using Cfg = LdsCfg<kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
+    build_group_table(a.gt, gl, E, Cfg::BM);
     if (!fast) {
         a.ntiles = (int)((Ncols + 255) / 256);
         const int64_t vblocks = a.M * a.ntiles;  // the kernels loop over virtual blocks past the grid
@@ -189,37 +171,29 @@ static void launch_gemm(GemmArgs& a, const int64_t* gl, int64_t E, int64_t batch
                 }
             }
         }
-        hipLaunchKernelGGL((skinny_kernel<EPI, kSkinnyPrefetch>), grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL((skinny_kernel<EPI>), grid, dim3(256), 0, st, a);
         return;
     }
     a.ntiles = (int)((EPI == EPI_SWIGLU) ? (Ncols + 127) / 128 : (Ncols + 255) / 256);
-    if (kUseLdsCore) {
-        using Cfg = LdsCfg<kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
-        build_group_table(a.gt, gl, E, Cfg::BM);
-        const int64_t blocks = (int64_t)a.gt.total_mtiles * a.ntiles;
-        const int pg = persistent_grid();
-        // persistent launch once there are more tiles than workgroups (one continuous DMA stream
-        // per workgroup: a tile's last STAGES iterations issue the next tile's first STAGES
-        // stages, so K must span at least STAGES stages); its register-direct epilogue addresses
-        // a tile's rows with 32-bit offsets
-        if constexpr (kPersistentGemm && EPI != EPI_SWIGLU) {
-            if (batch == 1 && pg > 0 && blocks > pg && a.K >= (int64_t)Cfg::STAGES_ * Cfg::BK &&
-                Cfg::BM * Ncols * 4 < 0x7fffffffLL) {
-                auto kern = lds_gemm_persistent_kernel<EPI, kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
-                constexpr int lds = Cfg::CONT_LDS_BYTES;  // the ring and two row-scale slots
-                allow_dynamic_lds((const void*)kern, lds);
-                hipLaunchKernelGGL(kern, dim3((unsigned)pg), dim3(Cfg::NT), lds, st, a);
-                return;
-            }
-        }
-        auto kern = lds_gemm_kernel<EPI, kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
-        allow_dynamic_lds((const void*)kern, Cfg::LDS_BYTES);
-        hipLaunchKernelGGL(kern, dim3((unsigned)blocks, (unsigned)batch), dim3(Cfg::NT), Cfg::LDS_BYTES, st, a);
-        return;
-    }
     const int64_t blocks = (int64_t)a.gt.total_mtiles * a.ntiles;
-    const dim3 grid((unsigned)blocks, (unsigned)batch);
-    hipLaunchKernelGGL((tiled_kernel<EPI, kTiledBM, 2>), grid, dim3(256), 0, st, a);
+    const int pg = persistent_grid();
+    // persistent launch once there are more tiles than workgroups (one continuous DMA stream per
+    // workgroup: a tile's last STAGES iterations issue the next tile's first STAGES stages, so K
+    // must span at least STAGES stages); its register-direct epilogue addresses a tile's rows with
+    // 32-bit offsets
+    if constexpr (EPI != EPI_SWIGLU) {
+        if (batch == 1 && pg > 0 && blocks > pg && a.K >= (int64_t)Cfg::STAGES_ * Cfg::BK &&
+            Cfg::BM * Ncols * 4 < 0x7fffffffLL) {
+            auto kern = lds_gemm_persistent_kernel<EPI, kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
+            constexpr int lds = Cfg::CONT_LDS_BYTES;  // the ring and two row-scale slots
+            allow_dynamic_lds((const void*)kern, lds);
+            hipLaunchKernelGGL(kern, dim3((unsigned)pg), dim3(Cfg::NT), lds, st, a);
+            return;
+        }
+    }
+    auto kern = lds_gemm_kernel<EPI, kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
+    allow_dynamic_lds((const void*)kern, Cfg::LDS_BYTES);
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks, (unsigned)batch), dim3(Cfg::NT), Cfg::LDS_BYTES, st, a);
 }
 
 }  // namespace cb
@@ -313,23 +287,35 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
     a.epi.yq = y;
     a.epi.yq_scale = y_scale;
 
+    a.epi.redo = (u32*)(wsb + ws.redo_off);
+    a.epi.spin_limit = g_overrides.exchange_spin_limit > 0 ? g_overrides.exchange_spin_limit : kExchangeSpins;
+
     const bool fast = K > 0 && K % 16 == 0 && H % 16 == 0 && offsets32_ok(K, N) && aligned(x, 16) &&
                       aligned(weight, 16) && aligned(act, 16) && aligned(weight_scale, 4);
-    if (fast && kUseLdsCore && kFusedRequant) {
-        // persistent GEMM with the requant fused: every column tile of a row tile is resident at once
-        build_group_table(a.gt, group_list, E, 256);
+    build_group_table(a.gt, group_list, E, 256);
+    if (fast && a.gt.max_rows > kSkinnyMaxRows && aligned(y, 4)) {
+        // persistent GEMM with the requant fused (prefill-shaped groups)
         const int ntl = (int)((H + 127) / 128);
         const int cus = device_cus();
-        if (a.gt.max_rows > kSkinnyMaxRows && cus >= ntl && a.gt.total_mtiles <= ws.n_arrive && aligned(y, 16)) {
-            const int slots = (ntl == 16 && cus >= 256) ? 16 : cus / ntl;  // 256 workgroups for 16 column tiles
+        const int grid = (ntl == 16 && cus >= 256) ? 256 : (cus / ntl) * ntl;
+        int resident = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, (const void*)gmsq_prefill_kernel, 256, kPfLds) !=
+            hipSuccess)
+            resident = 0;
+        // every workgroup of an exchange group must be resident at once: one per CU at most
+        if (grid >= ntl && resident >= 1 && a.gt.total_mtiles + 2 <= ws.n_arrive) {
             a.ntiles = ntl;
-            // amax, arrival counters and the status word are contiguous: one fill clears them
-            fill_u32(amax, (ws.status_off - ws.amax_off) / 4 + 1, 0u, st);
-            using Cfg = LdsCfg<kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
-            auto kern = lds_gemm_swiglu_q_kernel<kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
-            allow_dynamic_lds((const void*)kern, Cfg::LDS_BYTES);
-            TimedLaunch timed(st);
-            hipLaunchKernelGGL(kern, dim3((unsigned)(slots * ntl)), dim3(Cfg::NT), Cfg::LDS_BYTES, st, a);
+            // row maxima, arrival counters, the status word and the fix-up marks are contiguous
+            fill_u32(amax, (ws.redo_off - ws.amax_off) / 4 + (int64_t)a.gt.total_mtiles * ntl, 0u, st);
+            allow_dynamic_lds((const void*)gmsq_prefill_kernel, kPfLds);
+            allow_dynamic_lds((const void*)gmsq_prefill_fixup_kernel, kPfLds);
+            {
+                TimedLaunch timed(st);
+                hipLaunchKernelGGL(gmsq_prefill_kernel, dim3((unsigned)grid), dim3(256), kPfLds, st, a);
+            }
+            const int tiles = a.gt.total_mtiles * ntl;
+            hipLaunchKernelGGL(gmsq_prefill_fixup_kernel, dim3((unsigned)(tiles < 256 ? tiles : 256)), dim3(256), kPfLds,
+                               st, a);
             return check_launch();
         }
     }
@@ -513,14 +499,9 @@ extern "C" int cb_grouped_matmul_int32(const int8_t* x, const int8_t* weight, co
     return check_launch();
 }
 
-#ifdef CB_PROFILE
-extern "C" void cb_debug_profile(unsigned long long* out, int reset)
+extern "C" void cb_set_test_overrides(int persistent_grid, int exchange_spin_limit, int gmm_tile)
 {
-    (void)hipDeviceSynchronize();
-    (void)hipMemcpyFromSymbol(out, HIP_SYMBOL(cb_prof), sizeof(unsigned long long) * 8);
-    if (reset) {
-        unsigned long long z[8] = {0};
-        (void)hipMemcpyToSymbol(HIP_SYMBOL(cb_prof), z, sizeof(z));
-    }
+    g_overrides.persistent_grid = persistent_grid;
+    g_overrides.exchange_spin_limit = exchange_spin_limit;
+    g_overrides.gmm_tile = gmm_tile;
 }
-#endif

@@ -157,14 +157,28 @@ int cb_grouped_matmul_swiglu_quant_gather(const int8_t* x, int64_t x_rows, const
                                           int64_t workspace_bytes, void* stream);
 
 /*
- * Validation (no reference counterpart): the status word a GroupedMatmulSwigluQuant call left in
- * `workspace` (the same M, N, E).  0: every per-row maximum was complete when the row was
- * quantised.  1: a row-max exchange of the persistent kernel timed out (its workgroups could not
- * all be resident together within about 2 s) and some rows were quantised with a partial maximum.
- * Synchronises `stream`, so it is meant for tests and debug runs, not the hot loop.
+ * Diagnostics (no reference counterpart): the status word a GroupedMatmulSwigluQuant call left in
+ * `workspace` (the same M, N, E).  0: every row-maximum exchange completed in time.  1: some
+ * exchange wait gave up (its workgroups were not all resident together within the poll limit);
+ * the tiles concerned were recomputed by the fix-up launch with the final row maxima, so the
+ * outputs are right either way and only the time was lost.  Synchronises `stream`, so it is meant
+ * for tests and debug runs, not the hot loop.
  */
 int cb_grouped_matmul_swiglu_quant_status(const void* workspace, int64_t M, int64_t N, int64_t E,
                                           uint32_t* status, void* stream);
+
+/*
+ * Test hook (no reference counterpart; for this library's tests only).  Overrides for the calling
+ * thread's later launches, kept until changed; 0 restores each default:
+ *   persistent_grid      workgroups of the persistent dequant / int32 GEMM (default: the CU count;
+ *                        a small grid makes every workgroup walk many tiles); < 0 turns that
+ *                        persistent launch off.
+ *   exchange_spin_limit  polls of the GroupedMatmulSwigluQuant row-maximum exchange before a tile
+ *                        gives up and leaves its output to the fix-up launch (default 2^20, about
+ *                        2 s); a small value exercises the fix-up path.
+ *   gmm_tile             128 forces the 128 x 128 GroupedMatmul kernel for every fp16/bf16 shape.
+ */
+void cb_set_test_overrides(int persistent_grid, int exchange_spin_limit, int gmm_tile);
 
 /*
  * QuantMatmul (dense W8A8 with dequant epilogue).

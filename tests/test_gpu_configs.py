@@ -97,13 +97,20 @@ def test_gmsq_prefill_config4(cb, orc, prefill):
     experts, starts = _sample_experts(d["group_list"], 6, seed=2)
     ws = d["weight_scale"].cpu().numpy()
     xs = d["x_scale"].cpu().numpy()
+    def check(g, r0, r1):
+        yr, ysr = orc.gmsq(d["x"][r0:r1].cpu().numpy(), d["weight"][g:g + 1].cpu().numpy(), ws[g:g + 1],
+                           xs[r0:r1], np.array([r1 - r0]))
+        np.testing.assert_allclose(ysn[r0:r1], ysr, rtol=1e-5, err_msg=f"expert {g} rows {r0}:{r1}")
+        int8_close(yn[r0:r1], yr)
+
     for g in experts:
         s, e = starts[g], d["group_list"][g]
-        e2 = min(e, s + 700)
-        yr, ysr = orc.gmsq(d["x"][s:e2].cpu().numpy(), d["weight"][g:g + 1].cpu().numpy(), ws[g:g + 1],
-                           xs[s:e2], np.array([e2 - s]))
-        np.testing.assert_allclose(ysn[s:e2], ysr, rtol=1e-5, err_msg=f"expert {g}")
-        int8_close(yn[s:e2], yr)
+        check(g, s, min(e, s + 700))
+        if e - s > 700:
+            # the expert's last 256-row tile (partial unless the rows divide by 256) and the full
+            # tile before it: the group end inside a persistent tile
+            last = s + ((e - s - 1) // 256) * 256
+            check(g, max(s + 700, last - 256), e)
 
 
 def test_gmsq_prefill_every_row_vs_int32_core(cb, prefill):

@@ -67,10 +67,10 @@ CASES = [
 
 
 @pytest.fixture(params=["256", "128"])
-def gmm_tile(request, monkeypatch):
+def gmm_tile(request, overrides):
     """The 256 x 256 LDS-DMA kernel (default) and the 128 x 128 register-staged one."""
     if request.param == "128":
-        monkeypatch.setenv("CANNBENCH_AMD_GMM_TILE", "128")
+        overrides(gmm_tile=128)
     return request.param
 
 

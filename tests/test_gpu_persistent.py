@@ -1,7 +1,7 @@
 """GPU parity of the persistent dequant / int32 GEMM (one continuous DMA stage stream per workgroup).
 
 The default launch goes persistent only when a problem has more tiles than the device has CUs, so
-these tests force a small grid with CANNBENCH_AMD_PERSISTENT_GRID: every workgroup then walks many
+these tests force a small grid with the library's test override: every workgroup then walks many
 tiles.  Together the cases cover an odd number of K stages (the ring rotates between tiles), K of
 exactly the ring's depth, K shorter than the ring (launched one tile per workgroup instead), ragged
 and empty groups, partial row and column tiles, every dequant flag, and the last tile's stages that
@@ -31,8 +31,8 @@ def cpu_gen(seed):
 
 
 @pytest.fixture(params=[3, 5])
-def small_grid(request, monkeypatch):
-    monkeypatch.setenv("CANNBENCH_AMD_PERSISTENT_GRID", str(request.param))
+def small_grid(request, overrides):
+    overrides(persistent_grid=request.param)
     return request.param
 
 
@@ -107,7 +107,7 @@ def test_persistent_quant_matmul_flags(cb, orc, small_grid, variant):
     np.testing.assert_array_equal(bits16(out).reshape(ref.shape), ref)
 
 
-def test_persistent_default_grid_matches_one_tile_per_workgroup(cb, monkeypatch):
+def test_persistent_default_grid_matches_one_tile_per_workgroup(cb, overrides):
     """More tiles than CUs: the default launch is persistent; bit-identical to the launch with one
     tile per workgroup (persistent launch off) and to the oracle's int32 products on a sample."""
     g = cpu_gen(5)
@@ -121,7 +121,7 @@ def test_persistent_default_grid_matches_one_tile_per_workgroup(cb, monkeypatch)
     gl = np.cumsum(counts).tolist()
     a = cb.grouped_matmul_quant(x, w, ws, xs, gl)
     c = cb.grouped_matmul_int32(x, w, gl)
-    monkeypatch.setenv("CANNBENCH_AMD_PERSISTENT_GRID", "0")
+    overrides(persistent_grid=-1)  # persistent launch off: one tile per workgroup
     b = cb.grouped_matmul_quant(x, w, ws, xs, gl)
     d = cb.grouped_matmul_int32(x, w, gl)
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
