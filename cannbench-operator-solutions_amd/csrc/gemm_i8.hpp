@@ -1,24 +1,21 @@
-// gemm_i8.hpp - int8 x int8 -> int32 grouped GEMM cores for gfx950 with fused epilogues.
-//
-// All operators of the path share these cores:
-//   * GroupedMatmulSwigluQuant  (epilogue EPI_SWIGLU: per-token x per-channel dequant, SwiGLU with
-//     the gate in the left half, activation + per-row abs-max out; the int32 product never leaves
-//     the registers)
-//   * QuantMatmul and the int8 grouped down-projection (epilogue EPI_DEQUANT: the QuantMatmul
-//     dequant chain straight to bf16 / fp16)
+// gemm_i8.hpp - int8 x int8 -> int32 grouped GEMM: shared arguments, the skinny (decode) core and
+// the generic fallback kernels for gfx950.
 //
 // Weights are [E, K, N] with N contiguous (the reference layout, gmsq_launch.h:62-66).  The MFMA
-// B operand wants 16 consecutive K bytes per lane, so weight bytes are transposed in registers
-// with v_perm_b32 (4x4 byte blocks) on their way from HBM.
+// B operand wants 16 consecutive K bytes per lane, so the skinny core transposes weight bytes in
+// registers with v_perm_b32 (4x4 byte blocks) on their way from HBM.
 //
-// Two cores:
-//   skinny_kernel  decode-shaped groups (<= 16 rows per pass).  One workgroup = (group, 256
-//                  weight columns); its 4 waves split K, stream the weight block straight from
-//                  HBM into MFMA operands (v_mfma_i32_16x16x64_i8, no LDS staging for B) and
-//                  reduce their int32 partials through LDS.  Weight bytes are read exactly once.
-//   tiled_kernel   prefill / dense shapes.  BM x 256 x 64 tiles staged through double-buffered
-//                  LDS, v_mfma_i32_32x32x32_i8, an XCD-aware grouped tile order, and row blocks
-//                  past a group's end skipped wave-uniformly.
+//   skinny_kernel  decode-shaped groups (<= 16 rows per pass) of QuantMatmul and the int8 grouped
+//                  down-projection (EPI_DEQUANT: the QuantMatmul dequant chain straight to bf16 /
+//                  fp16) and the int32 GEMM (EPI_I32).  One workgroup = (group, 256 weight
+//                  columns); its 4 waves split K, stream the weight block straight from HBM into
+//                  MFMA operands (v_mfma_i32_16x16x64_i8, no LDS staging for B) and reduce their
+//                  int32 partials exactly through LDS.  Weight bytes are read exactly once.
+//                  GroupedMatmulSwigluQuant's decode kernel (gmsq_decode.hpp) shares its chunk
+//                  load and MFMA helpers.
+//   generic_*      any K / N / alignment, one thread per output (correctness path only).
+// The prefill / dense LDS core is in gemm_lds.hpp, the GroupedMatmulSwigluQuant prefill kernel in
+// gmsq_prefill.hpp.
 #pragma once
 
 #include "common.hpp"
@@ -26,7 +23,7 @@
 
 namespace cb {
 
-enum { EPI_SWIGLU = 0, EPI_DEQUANT = 1, EPI_I32 = 2 };
+enum { EPI_DEQUANT = 1, EPI_I32 = 2 };
 
 enum { BIAS_NONE = 0, BIAS_I32 = 1, BIAS_F16 = 2, BIAS_BF16 = 3, BIAS_F32 = 4 };
 
@@ -38,10 +35,12 @@ enum { BIAS_NONE = 0, BIAS_I32 = 1, BIAS_F16 = 2, BIAS_BF16 = 3, BIAS_F32 = 4 };
 //   [v *= pertoken[row]]; [v += bias (float kinds)]; out = round16(v)
 // scale may be offset per group (scale_gstride elements) for the grouped down-projection.
 //
-// EPI_SWIGLU computes, like the reference GMSQ vector stage (gmsq_vec_kernel.cpp:15-20, 207-231):
+// GroupedMatmulSwigluQuant's epilogue computes, like the reference GMSQ vector stage
+// (gmsq_vec_kernel.cpp:15-20, 207-257):
 //   L = (float(c[j]) * xs[i]) * ws[g, j], R = (float(c[j+H]) * xs[i]) * ws[g, j+H]
-//   act = (L / (1 + exp(-L))) * R, stored fp32, and the running |act| max per row (atomic, as the
-//   bit pattern of a non-negative float).
+//   act = (L / (1 + exp(-L))) * R;  amax = max |act| over the row (the bit pattern of a
+//   non-negative float, combined across tiles with atomics), floored at FLT_MIN;
+//   y = rint16(act * 127 / amax), y_scale = amax / 127.
 struct EpiArgs {
     const void* scale;
     int64_t scale_gstride;
@@ -62,7 +61,6 @@ struct EpiArgs {
     // SwiGLU
     const float* w_scale;
     const float* x_scale;
-    float* act;
     u32* amax;
     int64_t H;
     // fused requant (the persistent prefill kernel, gmsq_prefill.hpp)
@@ -263,32 +261,7 @@ __device__ __forceinline__ void skinny_row_epilogue(const GemmArgs& a, const int
     const int64_t N = a.N;
     const EpiArgs& e = a.epi;
     (void)col;
-    if constexpr (EPI == EPI_SWIGLU) {
-        const int64_t H = e.H;
-        int u[16];  // the up-projection partner column sits 8 lanes away
-#pragma unroll
-        for (int j = 0; j < 16; ++j) u[j] = __shfl_xor(s[j], 8, 64);
-        float m = 0.0f;
-        if (c < 8 && rowok && colok) {
-            const float xs = src_x_scale(a, row);
-            const float* wsg = e.w_scale + (int64_t)g * N + opaque(ocol);
-            const float* wsu = wsg + H;
-            float act[16];
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                act[j] = swiglu((float)s[j], (float)u[j], xs, wsg[j], wsu[j]);
-                m = fmaxf(m, fabsf(act[j]));
-            }
-            float4* dst = reinterpret_cast<float4*>(e.act + (int64_t)row * H + ocol);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                dst[j] = make_float4(act[4 * j], act[4 * j + 1], act[4 * j + 2], act[4 * j + 3]);
-        }
-        m = fmaxf(m, __shfl_xor(m, 1, 64));
-        m = fmaxf(m, __shfl_xor(m, 2, 64));
-        m = fmaxf(m, __shfl_xor(m, 4, 64));
-        if (c == 0 && rowok) atomicMax(e.amax + row, __float_as_uint(m));
-    } else if constexpr (EPI == EPI_I32) {
+    if constexpr (EPI == EPI_I32) {
         if (rowok && colok) {
             int4* dst = reinterpret_cast<int4*>((int32_t*)e.out + b * e.out_bstride + (int64_t)row * N + ocol);
 #pragma unroll
@@ -312,6 +285,23 @@ __device__ __forceinline__ void skinny_row_epilogue(const GemmArgs& a, const int
     }
 }
 
+// Block -> (group, column tile) of the skinny kernels.  a.xcd_split = P > 0: XCD pair / quad p
+// streams groups p, p + 8 / P, ... and each of its P XCDs one contiguous 1 / P of their column
+// tiles (workgroups are dispatched round-robin over the 8 XCDs in linear block order).
+__device__ __forceinline__ void skinny_block(const GemmArgs& a, int& g, int& ct)
+{
+    g = blockIdx.y;
+    ct = blockIdx.x;
+    const int P = a.xcd_split;
+    if (P > 0) {
+        const int G = 8 / P;
+        const int lin = blockIdx.y * gridDim.x + blockIdx.x;
+        const int x = lin & 7, j = lin >> 3, h = gridDim.x / P;
+        g = (j / h) * G + x / P;
+        ct = (x % P) * h + j % h;
+    }
+}
+
 // ============================================================================================
 // skinny_kernel: decode-shaped groups.
 //   grid = (ntiles, E), block = 256 (4 waves).  SwiGLU tiles cover 128 gate + 128 up columns,
@@ -330,15 +320,8 @@ __global__ __launch_bounds__(256, 2) void skinny_kernel(const GemmArgs a)
     // (16 column tiles) or 3.5 KB (28) run of each weight row instead of two scattered 256-byte
     // pieces.  Measured on a weight-streaming probe: 6.3 vs 5.5 TB/s.  Needs an even tile count
     // and a group count divisible by 4 (the host passes the grid as is otherwise).
-    int g = blockIdx.y, ct = blockIdx.x;
-    const int P = a.xcd_split;  // XCDs sharing one group's column tiles (0: identity order)
-    if (P > 0) {
-        const int G = 8 / P;
-        const int lin = blockIdx.y * gridDim.x + blockIdx.x;
-        const int x = lin & 7, j = lin >> 3, h = gridDim.x / P;
-        g = (j / h) * G + x / P;
-        ct = (x % P) * h + j % h;
-    }
+    int g, ct;
+    skinny_block(a, g, ct);
     const int r0 = g ? a.gt.row_end[g - 1] : 0;
     const int r1 = a.gt.row_end[g];
     if (r0 >= r1) return;
@@ -348,19 +331,9 @@ __global__ __launch_bounds__(256, 2) void skinny_kernel(const GemmArgs a)
     const int64_t K = a.K, N = a.N;
     const EpiArgs& e = a.epi;
 
-    int64_t col;   // first weight column of this lane's group
-    int64_t ocol;  // first output column (act column for SwiGLU)
-    bool colok;
-    if constexpr (EPI == EPI_SWIGLU) {
-        const int64_t H = e.H;
-        ocol = (int64_t)ct * 128 + 16 * (c & 7);
-        colok = ocol < H;
-        col = (c < 8) ? ocol : H + ocol;
-    } else {
-        ocol = (int64_t)ct * 256 + 16 * c;
-        colok = ocol < N;
-        col = ocol;
-    }
+    const int64_t ocol = (int64_t)ct * 256 + 16 * c;  // first weight / output column of this lane
+    const bool colok = ocol < N;
+    const int64_t col = ocol;
     const int64_t b = blockIdx.z;  // batch (dense QuantMatmul)
     // weight block of this group (the host sends K * N >= 2^31 to the generic kernels)
     const __amdgpu_buffer_rsrc_t wres = make_rsrc(a.w + b * a.w_bstride + (int64_t)g * a.w_gstride, (uint32_t)(K * N));
@@ -452,6 +425,10 @@ __device__ __forceinline__ int group_of_row(const GroupTable& gt, int row)
 
 // The generic kernels walk virtual blocks vb = (row, 256-column tile) with a grid-stride loop, so
 // any M x tiles count fits a launch (a dispatch counts its work-items in 32 bits).
+// GroupedMatmulSwigluQuant for shapes off the vector paths, in two passes over the same products
+// (no intermediate in memory): QUANT = false publishes the per-row |act| maxima, QUANT = true
+// recomputes act and writes y = rint16(act * 127 / amax) and y_scale (column tile 0, thread 0).
+template <bool QUANT>
 static __global__ __launch_bounds__(256) void generic_swiglu_kernel(const GemmArgs a)
 {
     const int64_t H = a.epi.H;
@@ -474,10 +451,16 @@ static __global__ __launch_bounds__(256) void generic_swiglu_kernel(const GemmAr
             }
             v = swiglu((float)cg, (float)cu, src_x_scale(a, row), a.epi.w_scale[(int64_t)g * a.N + idx],
                        a.epi.w_scale[(int64_t)g * a.N + H + idx]);
-            a.epi.act[(int64_t)row * H + idx] = v;
         }
-        const float m = wave_max(ok ? fabsf(v) : 0.0f);
-        if ((threadIdx.x & 63) == 0) atomicMax(a.epi.amax + row, __float_as_uint(m));
+        if constexpr (!QUANT) {
+            const float m = wave_max(ok ? fabsf(v) : 0.0f);
+            if ((threadIdx.x & 63) == 0) atomicMax(a.epi.amax + row, __float_as_uint(m));
+        } else {
+            float am = __uint_as_float(a.epi.amax[row]);
+            if (!(am > kFltMin)) am = kFltMin;
+            if (ok) a.epi.yq[(int64_t)row * H + idx] = (int8_t)rint16(v * (127.0f / am));
+            if (vb % a.ntiles == 0 && threadIdx.x == 0) a.epi.yq_scale[row] = am * kInv127;
+        }
     }
 }
 

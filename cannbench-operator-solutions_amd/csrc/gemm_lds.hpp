@@ -203,7 +203,7 @@ struct TileDma {
 };
 
 template <int EPI, int WM, int WN, int STAGES, int BKT>
-using TileDmaOf = TileDma<LdsCfg<WM, WN, STAGES, BKT>, EPI == EPI_SWIGLU>;
+using TileDmaOf = TileDma<LdsCfg<WM, WN, STAGES, BKT>, false>;
 
 // One 256 x 256 output tile (row tile mt, column tile nt, batch b).  Called once per workgroup by
 // lds_gemm_kernel and in a loop by the persistent kernels.
@@ -220,7 +220,6 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
                                               const int sbase = 0, const int xs_slot = 0)
 {
     using C = LdsCfg<WM, WN, STAGES, BKT>;
-    constexpr bool SW = EPI == EPI_SWIGLU;
     constexpr int KS = C::KS, ACH = C::ACH;
     constexpr int BM = C::BM, BN = C::BN, BK = C::BK, TN = C::TN, FM = C::FM,
                   FN = C::FN;
@@ -236,8 +235,8 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
     const int m0 = rs + (mt - a.gt.tile_start[g]) * BM;
     const int vrows = r1 - m0;  // valid rows of this tile (>= 1)
 
-    static_assert(!(CONT && SW), "continuous stage stream: dequant / int32 epilogues only");
-    TileDma<C, SW> dma;
+    static_assert(EPI == EPI_DEQUANT || EPI == EPI_I32, "dequant / int32 epilogues only");
+    TileDma<C, false> dma;
     if constexpr (CONT) dma = *cur;
     else dma.init(a, mt, nt, b, wave, lane);
     const uint32_t lds_base = (uint32_t)(uintptr_t)(CB_LDS uint8_t*)smem;
@@ -254,12 +253,7 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
         }
     };
 
-    auto tcol = [&](int fn) -> int {  // first tile column of wave fragment fn
-        if constexpr (SW)
-            return fn < FN / 2 ? wn * (TN / 2) + fn * 32 : BN / 2 + wn * (TN / 2) + (fn - FN / 2) * 32;
-        else
-            return wn * TN + fn * 32;
-    };
+    auto tcol = [&](int fn) -> int { return wn * TN + fn * 32; };  // first tile column of fragment fn
 
     // ---- per-lane LDS read offsets ----------------------------------------------------------
     // A: fragment fm of wave row wm covers tile rows 32 (WM fm + wm) .. +32 (row blocks are
@@ -312,23 +306,12 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
         for (int st = 0; st < STAGES; ++st) issue_stage(st);
     }
     // Scales of the epilogue, fetched now so the loads hide under the K loop; the epilogue reads
-    // them from LDS.  Row scales (SwiGLU: the activation scale, through the row index when
-    // gathered; dequant: the per-token scale, 1 without one): thread tid takes tile row tid % BM.
-    // Column scales (SwiGLU: w_scale of the 128 gate then the 128 up columns; dequant: the output
-    // scale): thread tid takes tile column tid % BN.  Every thread loads, with no branch around a
-    // load: absent operands read through empty buffer resources.
+    // them from LDS.  Row scales (the per-token scale, 1 without one): thread tid takes tile row
+    // tid % BM.  Column scales (the output scale): thread tid takes tile column tid % BN.  Every
+    // thread loads, with no branch around a load: absent operands read through empty buffer
+    // resources.
     float xs_pre = 1.0f, cs_pre = 0.0f;
-    if constexpr (SW) {
-        const int xr = m0 + tid % BM;
-        xs_pre = src_x_scale(a, xr < r1 ? xr : r1 - 1);
-        const int64_t H = e.H;
-        const int j = tid % BN;
-        const int64_t jc = (int64_t)nt * (BN / 2) + (j & (BN / 2 - 1));
-        const int64_t wc = j < BN / 2 ? jc : H + jc;
-        const __amdgpu_buffer_rsrc_t wsr = make_rsrc(e.w_scale + (int64_t)g * N, (uint32_t)(N * 4));
-        cs_pre = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                               wsr, jc < H ? (uint32_t)(wc * 4) : 0x80000000u, 0, 0));
-    } else if constexpr (EPI == EPI_DEQUANT) {
+    if constexpr (EPI == EPI_DEQUANT) {
         const int lr0 = tid % BM;
         const __amdgpu_buffer_rsrc_t pres =
             e.has_pt ? make_rsrc(e.pertoken + m0, (uint32_t)((vrows < BM ? vrows : BM) * 4)) : make_rsrc(a.x, 0u);
@@ -522,57 +505,6 @@ __device__ __forceinline__ void lds_gemm_tile(const GemmArgs& a, const int mt, c
             else
                 store(std::integral_constant<bool, false>());
         }
-    } else if constexpr (SW) {
-        // act tile [256 rows][128 act columns] fp32 staged in LDS, then written with 16-byte stores
-        // and one row-max atomic per (row, tile)
-        const int64_t H = e.H;
-        publish_scales();  // published by the barrier below
-        epi_barrier();
-        float wsg[FN / 2], wsu[FN / 2];  // 0 past H
-#pragma unroll
-        for (int fn = 0; fn < FN / 2; ++fn) {
-            wsg[fn] = cs_lds[wn * (TN / 2) + fn * 32 + (lane & 31)];
-            wsu[fn] = cs_lds[BN / 2 + wn * (TN / 2) + fn * 32 + (lane & 31)];
-        }
-        CB_LDS uint8_t* st = (CB_LDS uint8_t*)smem;
-#pragma unroll
-        for (int fm = 0; fm < FM; ++fm) {
-            if (!fvalid[fm]) continue;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int lrow = (WM * fm + wm) * 32 + (r >> 2) * 8 + lr + (r & 3);
-                const float xs = xs_lds[lrow];  // row min(m0 + lrow, r1 - 1)'s scale
-#pragma unroll
-                for (int fn = 0; fn < FN / 2; ++fn) {
-                    const float v = swiglu((float)acc[fm][fn][r], (float)acc[fm][fn + FN / 2][r], xs, wsg[fn], wsu[fn]);
-                    const int lcol = wn * (TN / 2) + fn * 32 + (lane & 31);
-                    *(CB_LDS float*)(st + lrow * C::EPI_PITCH + lcol * 4) = v;
-                }
-            }
-        }
-        epi_barrier();
-        // two threads per row, 64 act columns (16 x float4) each
-        constexpr int TPR = C::NT / BM;           // threads per row
-        constexpr int CPT = (BN / 2) / TPR;       // act columns per thread
-        const int lrow = tid / TPR, part = tid % TPR;
-        const int row = m0 + lrow;
-        const int64_t j0 = (int64_t)nt * (BN / 2) + part * CPT;
-        const CB_LDS v4f* src = (const CB_LDS v4f*)(st + lrow * C::EPI_PITCH + part * CPT * 4);
-        float m = 0.0f;
-        if (row < r1) {
-            v4f* dst = reinterpret_cast<v4f*>(e.act + (int64_t)row * H + j0);
-#pragma unroll
-            for (int i = 0; i < CPT / 4; ++i) {
-                if (j0 + 4 * i < H) {
-                    const v4f v = src[i];
-                    dst[i] = v;
-                    m = fmaxf(m, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
-                }
-            }
-        }
-#pragma unroll
-        for (int o = 1; o < TPR; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        if (part == 0 && row < r1) atomicMax(e.amax + row, __float_as_uint(m));
     } else if constexpr (EPI == EPI_I32) {
         int32_t* ob = (int32_t*)e.out + b * e.out_bstride;
 #pragma unroll

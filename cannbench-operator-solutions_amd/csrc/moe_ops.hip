@@ -10,44 +10,10 @@
 #include <set>
 #include <utility>
 
+#include "gmsq_decode.hpp"
 #include "gmsq_prefill.hpp"
 
 namespace cb {
-
-// Phase 2 of GroupedMatmulSwigluQuant: per-token requant of the fp32 activation with the row
-// abs-max accumulated by the GEMM epilogue (gmsq_vec_kernel.cpp:233-257):
-//   amax <- FLT_MIN unless amax > FLT_MIN;  y_scale = amax * (1/127)
-//   y = rint16(clamp(act * (127 / amax), -128, 127))   (rint16 saturates)
-__device__ __forceinline__ void gmsq_requant_row(const float* __restrict__ act, const u32* __restrict__ amax,
-                                                 const int64_t row, const int64_t H, int8_t* __restrict__ y,
-                                                 float* __restrict__ ys)
-{
-    float a = __uint_as_float(amax[row]);
-    if (!(a > kFltMin)) a = kFltMin;
-    if (threadIdx.x == 0) ys[row] = a * kInv127;
-    const float inv = 127.0f / a;
-    const float* src = act + row * H;
-    int8_t* dst = y + row * H;
-    // clamp(v, -128, 127) then narrow == saturating rint16 for every non-NaN v; an all-zero row
-    // gives 0 * inf = NaN, which rint16 maps to 0
-    auto q = [&](float v) { return rint16(v * inv); };
-    if ((H & 3) == 0) {
-        for (int64_t j = (int64_t)threadIdx.x * 4; j < H; j += 1024) {
-            const float4 v = *reinterpret_cast<const float4*>(src + j);
-            *reinterpret_cast<u32*>(dst + j) = pack4_i8(q(v.x), q(v.y), q(v.z), q(v.w));
-        }
-    } else {
-        for (int64_t j = threadIdx.x; j < H; j += 256) dst[j] = (int8_t)q(src[j]);
-    }
-}
-
-// Rows blockIdx.x + i * gridDim.x: the grid is capped, since a dispatch counts its work-items in 32 bits.
-__global__ __launch_bounds__(256) void gmsq_requant_kernel(const float* __restrict__ act,
-                                                           const u32* __restrict__ amax, int64_t M, int64_t H,
-                                                           int8_t* __restrict__ y, float* __restrict__ ys)
-{
-    for (int64_t row = blockIdx.x; row < M; row += gridDim.x) gmsq_requant_row(act, amax, row, H, y, ys);
-}
 
 __global__ void fill_u32_kernel(u32* p, int64_t n, u32 v)
 {
@@ -64,26 +30,30 @@ static void fill_u32(u32* p, int64_t n, u32 v, hipStream_t st)
 
 static inline int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
-// Workspace layout of GroupedMatmulSwigluQuant: u32 row abs-max [M], u32 arrival counters (one per
-// exchange round; at most M / 256 + E + 2 rounds), a u32 status word, u32 fix-up marks (one per
-// 256-row x 128-column tile), then the fp32 activation [M, H] that only the non-persistent paths
-// (decode-shaped groups, unaligned shapes) write.
+// Workspace layout of GroupedMatmulSwigluQuant (all u32): the row |act| maxima (prefill: one per
+// row, M words; decode: one marked slot per (row, 128-column tile), at most 32 E rows x ntiles),
+// arrival counters (prefill: one per exchange round, at most M / 256 + E + 2), the status word and
+// the decode kernel's tile tickets (256 bytes), then the fix-up marks (prefill: one per 256-row x
+// 128-column tile; decode: one per (expert, column tile)).  No intermediate product or activation
+// is ever stored: M = 131072 rows need about 0.7 MB.
 struct GmsqWorkspace {
-    int64_t amax_off, arrive_off, status_off, redo_off, act_off, total, n_arrive, n_redo;
+    int64_t amax_off, arrive_off, status_off, redo_off, total, n_arrive, n_redo;
 };
 
 static GmsqWorkspace gmsq_workspace(int64_t M, int64_t N, int64_t E)
 {
     GmsqWorkspace w;
     const int64_t H = N / 2;
+    const int64_t ntl = (H + 127) / 128;
+    const int64_t dec_rows = M < 32 * E ? M : 32 * E;  // decode-shaped groups hold at most 32 rows
+    const int64_t n_amax = M > dec_rows * ntl ? M : dec_rows * ntl;
     w.n_arrive = M / 256 + E + 2;
-    w.n_redo = (M / 256 + E) * ((H + 127) / 128);
+    w.n_redo = (M / 256 + E) * ntl;
     w.amax_off = 0;
-    w.arrive_off = round_up(M * 4, 256);
+    w.arrive_off = round_up(n_amax * 4, 256);
     w.status_off = w.arrive_off + round_up(w.n_arrive * 4, 256);
     w.redo_off = w.status_off + 256;
-    w.act_off = w.redo_off + round_up(w.n_redo * 4, 256);
-    w.total = w.act_off + round_up(M * H * 4, 256);
+    w.total = w.redo_off + round_up(w.n_redo * 4, 256);
     return w;
 }
 
@@ -137,59 +107,60 @@ static constexpr int kLdsWM = 4, kLdsWN = 2, kLdsStages = 2, kLdsBK = 128;
 
 thread_local KernelTiming g_timing;
 
+// XCD split of the skinny kernels: the most XCDs per group (4, 2, 1) that divide the column tiles
+// and still give each XCD runs of at least 1 KB per weight row (measured best: decode 2,
+// down-projection 4); 0 keeps the plain block order.
+static int xcd_split(int ntiles, int64_t E, int64_t tile_row_bytes)
+{
+    for (int P = 4; P >= 1; P >>= 1)
+        if (ntiles % P == 0 && E % (8 / P) == 0 && (ntiles / P) * tile_row_bytes >= 1024) return P;
+    return 0;
+}
+
 template <int EPI>
 static void launch_gemm(GemmArgs& a, const int64_t* gl, int64_t E, int64_t batch, bool fast, hipStream_t st)
 {
     TimedLaunch timed(st);
-    const int64_t Ncols = (EPI == EPI_SWIGLU) ? a.epi.H : a.N;  // output columns
+    static_assert(EPI == EPI_DEQUANT || EPI == EPI_I32, "GroupedMatmulSwigluQuant has its own kernels");
+    const int64_t Ncols = a.N;  // output columns
     using Cfg = LdsCfg<kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
     build_group_table(a.gt, gl, E, Cfg::BM);
     if (!fast) {
         a.ntiles = (int)((Ncols + 255) / 256);
         const int64_t vblocks = a.M * a.ntiles;  // the kernels loop over virtual blocks past the grid
         const dim3 grid((unsigned)(vblocks < (1 << 20) ? vblocks : (1 << 20)), (unsigned)batch);
-        if constexpr (EPI == EPI_SWIGLU)
-            hipLaunchKernelGGL(generic_swiglu_kernel, grid, dim3(256), 0, st, a);
-        else if constexpr (EPI == EPI_I32)
+        if constexpr (EPI == EPI_I32)
             hipLaunchKernelGGL(generic_i32_kernel, grid, dim3(256), 0, st, a);
         else
             hipLaunchKernelGGL(generic_dequant_kernel, grid, dim3(256), 0, st, a);
         return;
     }
     if (a.gt.max_rows <= kSkinnyMaxRows) {
-        a.ntiles = (int)((EPI == EPI_SWIGLU) ? (Ncols + 127) / 128 : (Ncols + 255) / 256);
+        a.ntiles = (int)((Ncols + 255) / 256);
         const dim3 grid((unsigned)a.ntiles, (unsigned)E, (unsigned)batch);
         // XCD split: the most XCDs per group (4, 2, 1) that divide the column tiles and still give
         // each XCD runs of at least 1 KB per weight row (measured best: decode 2, down-projection 4)
         a.xcd_split = 0;
         if (batch == 1) {
-            const int64_t tile_row_bytes = EPI == EPI_SWIGLU ? 128 : 256;
-            for (int P = 4; P >= 1; P >>= 1) {
-                if (a.ntiles % P == 0 && E % (8 / P) == 0 && (a.ntiles / P) * tile_row_bytes >= 1024) {
-                    a.xcd_split = P;
-                    break;
-                }
-            }
+            a.xcd_split = xcd_split(a.ntiles, E, 256);
         }
         hipLaunchKernelGGL((skinny_kernel<EPI>), grid, dim3(256), 0, st, a);
         return;
     }
-    a.ntiles = (int)((EPI == EPI_SWIGLU) ? (Ncols + 127) / 128 : (Ncols + 255) / 256);
+    a.ntiles = (int)((Ncols + 255) / 256);
     const int64_t blocks = (int64_t)a.gt.total_mtiles * a.ntiles;
     const int pg = persistent_grid();
     // persistent launch once there are more tiles than workgroups (one continuous DMA stream per
     // workgroup: a tile's last STAGES iterations issue the next tile's first STAGES stages, so K
     // must span at least STAGES stages); its register-direct epilogue addresses a tile's rows with
     // 32-bit offsets
-    if constexpr (EPI != EPI_SWIGLU) {
-        if (batch == 1 && pg > 0 && blocks > pg && a.K >= (int64_t)Cfg::STAGES_ * Cfg::BK &&
-            Cfg::BM * Ncols * 4 < 0x7fffffffLL) {
-            auto kern = lds_gemm_persistent_kernel<EPI, kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
-            constexpr int lds = Cfg::CONT_LDS_BYTES;  // the ring and two row-scale slots
-            allow_dynamic_lds((const void*)kern, lds);
-            hipLaunchKernelGGL(kern, dim3((unsigned)pg), dim3(Cfg::NT), lds, st, a);
-            return;
-        }
+    if (batch == 1 && pg > 0 && blocks > pg && a.K >= (int64_t)Cfg::STAGES_ * Cfg::BK &&
+        Cfg::BM * Ncols * 4 < 0x7fffffffLL) {
+        auto kern = lds_gemm_persistent_kernel<EPI, kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
+        constexpr int lds = Cfg::CONT_LDS_BYTES;  // the ring and two row-scale slots
+        allow_dynamic_lds((const void*)kern, lds);
+        hipLaunchKernelGGL(kern, dim3((unsigned)pg), dim3(Cfg::NT), lds, st, a);
+        return;
     }
     auto kern = lds_gemm_kernel<EPI, kLdsWM, kLdsWN, kLdsStages, kLdsBK>;
     allow_dynamic_lds((const void*)kern, Cfg::LDS_BYTES);
@@ -261,10 +232,7 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
     hipStream_t st = (hipStream_t)stream;
     const int64_t H = N / 2;
     uint8_t* wsb = (uint8_t*)workspace;
-    float* act = (float*)(wsb + ws.act_off);
     u32* amax = (u32*)(wsb + ws.amax_off);
-    u32* arrive = (u32*)(wsb + ws.arrive_off);
-    u32* status = (u32*)(wsb + ws.status_off);
 
     GemmArgs a;
     std::memset(&a, 0, sizeof(a));
@@ -278,24 +246,24 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
     a.x_rows = row_index ? x_rows : M;
     a.epi.w_scale = weight_scale;
     a.epi.x_scale = x_scale;
-    a.epi.act = act;
     a.epi.amax = amax;
     a.epi.H = H;
-
-    a.epi.arrive = arrive;
-    a.epi.status = status;
+    a.epi.arrive = (u32*)(wsb + ws.arrive_off);
+    a.epi.status = (u32*)(wsb + ws.status_off);
+    a.epi.redo = (u32*)(wsb + ws.redo_off);
     a.epi.yq = y;
     a.epi.yq_scale = y_scale;
-
-    a.epi.redo = (u32*)(wsb + ws.redo_off);
     a.epi.spin_limit = g_overrides.exchange_spin_limit > 0 ? g_overrides.exchange_spin_limit : kExchangeSpins;
+    build_group_table(a.gt, group_list, E, 256);
+    // row maxima, arrival counters, the status word and the fix-up marks are contiguous: one fill
+    // clears what this call's launches use
+    auto clear_ws = [&](int64_t n_redo) { fill_u32(amax, (ws.redo_off - ws.amax_off) / 4 + n_redo, 0u, st); };
 
     const bool fast = K > 0 && K % 16 == 0 && H % 16 == 0 && offsets32_ok(K, N) && aligned(x, 16) &&
-                      aligned(weight, 16) && aligned(act, 16) && aligned(weight_scale, 4);
-    build_group_table(a.gt, group_list, E, 256);
+                      aligned(weight, 16) && aligned(weight_scale, 4);
+    const int ntl = (int)((H + 127) / 128);  // 128-act-column tiles
     if (fast && a.gt.max_rows > kSkinnyMaxRows && aligned(y, 4)) {
-        // persistent GEMM with the requant fused (prefill-shaped groups)
-        const int ntl = (int)((H + 127) / 128);
+        // prefill-shaped groups: the persistent GEMM with the requant fused
         const int cus = device_cus();
         const int grid = (ntl == 16 && cus >= 256) ? 256 : (cus / ntl) * ntl;
         int resident = 0;
@@ -305,8 +273,7 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
         // every workgroup of an exchange group must be resident at once: one per CU at most
         if (grid >= ntl && resident >= 1 && a.gt.total_mtiles + 2 <= ws.n_arrive) {
             a.ntiles = ntl;
-            // row maxima, arrival counters, the status word and the fix-up marks are contiguous
-            fill_u32(amax, (ws.redo_off - ws.amax_off) / 4 + (int64_t)a.gt.total_mtiles * ntl, 0u, st);
+            clear_ws((int64_t)a.gt.total_mtiles * ntl);
             allow_dynamic_lds((const void*)gmsq_prefill_kernel, kPfLds);
             allow_dynamic_lds((const void*)gmsq_prefill_fixup_kernel, kPfLds);
             {
@@ -319,11 +286,39 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
             return check_launch();
         }
     }
-    // row maxima and the status word start at zero on this path too
-    fill_u32(amax, (ws.status_off - ws.amax_off) / 4 + 2, 0u, st);
-    launch_gemm<EPI_SWIGLU>(a, group_list, E, 1, fast, st);
-    hipLaunchKernelGGL(gmsq_requant_kernel, dim3((unsigned)(M < 65536 ? M : 65536)), dim3(256), 0, st, act, amax, M,
-                       H, y, y_scale);
+    if (fast && a.gt.max_rows <= kSkinnyMaxRows && aligned(y, 16)) {
+        // decode-shaped groups: weight streaming with the requant fused (per-expert exchange), on a
+        // persistent grid of two workgroups per CU drawing tiles from per-XCD lists
+        const int cus = device_cus();
+        int resident = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, (const void*)gmsq_decode_kernel, 256, 0) !=
+            hipSuccess)
+            resident = 0;
+        const int64_t tiles = E * ntl;
+        int grid = (resident < 2 ? resident : 2) * cus;
+        if (grid > tiles) grid = (int)tiles;
+        if (grid >= 1) {
+            a.ntiles = ntl;
+            const int xcd_lists = 0;  // measured: one list in expert order beats per-XCD lists
+            clear_ws(tiles);
+            {
+                TimedLaunch timed(st);
+                hipLaunchKernelGGL(gmsq_decode_kernel, dim3((unsigned)grid), dim3(256), 0, st, a, xcd_lists);
+            }
+            hipLaunchKernelGGL(gmsq_decode_fixup_kernel, dim3((unsigned)(tiles < 512 ? tiles : 512)), dim3(256), 0, st, a);
+            return check_launch();
+        }
+    }
+    // any other shape or alignment: two passes over the products (row maxima, then the requant)
+    clear_ws(0);
+    a.ntiles = (int)((H + 255) / 256);
+    const int64_t vblocks = M * a.ntiles;  // the kernels loop over virtual blocks past the grid
+    const dim3 grid((unsigned)(vblocks < (1 << 20) ? vblocks : (1 << 20)));
+    {
+        TimedLaunch timed(st);
+        hipLaunchKernelGGL(generic_swiglu_kernel<false>, grid, dim3(256), 0, st, a);
+    }
+    hipLaunchKernelGGL(generic_swiglu_kernel<true>, grid, dim3(256), 0, st, a);
     return check_launch();
 }
 

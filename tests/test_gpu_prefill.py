@@ -1,4 +1,5 @@
-"""The persistent GroupedMatmulSwigluQuant prefill kernel's failure handling and 32-bit limits.
+"""Failure handling of the fused GroupedMatmulSwigluQuant kernels (prefill and decode) and the
+32-bit limits of the GEMM cores.
 
 * The row-maximum exchange wait is bounded.  A test override shrinks the poll limit so that the
   kernel's own wait gives up on most tiles (every kernel still exits normally); the fix-up launch
@@ -64,8 +65,10 @@ def _run_raw(cb, x, w, ws, xs, gl):
 
 
 @pytest.mark.parametrize("counts,K,N", [
-    ([300, 0, 700, 45, 1000], 512, 4096),   # 16 column tiles: the 256-workgroup grid, 4 row tiles per round
-    ([260, 33, 513], 384, 1024),            # 4 column tiles: one row tile per exchange group
+    ([300, 0, 700, 45, 1000], 512, 4096),   # prefill, 16 column tiles: the 256-workgroup grid, 4 row tiles per round
+    ([260, 33, 513], 384, 1024),            # prefill, 4 column tiles: one row tile per exchange group
+    ([5, 0, 17, 32, 1, 9] * 8, 448, 4096),  # decode: at most 32 rows per expert, 16 column tiles
+    ([3, 31, 0, 12], 320, 1056),            # decode: 5 column tiles, the last one partial
 ])
 def test_exchange_timeout_fixup(cb, orc, overrides, counts, K, N):
     x, w, ws, xs, gl = _inputs(counts, K, N, sum(counts) + K)
