@@ -149,8 +149,7 @@ __device__ __forceinline__ bool decode_gather(const GemmArgs& a, const int r0, c
             am[rb] = __uint_as_float(m);
             all = all && ok;
         }
-        // wave-uniform decision
-        if (__builtin_amdgcn_readfirstlane((int)__builtin_amdgcn_ballot_w64(!all) == 0 ? 1 : 0)) return true;
+        if (__builtin_amdgcn_ballot_w64(!all) == 0) return true;  // all 64 lanes' rows are final
         if (spins >= a.epi.spin_limit) return false;
         __builtin_amdgcn_s_sleep(4);
     }
@@ -234,6 +233,8 @@ __global__ __launch_bounds__(256, 2) void gmsq_decode_kernel(const GemmArgs a, c
     if (threadIdx.x == 0) next_t = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     int t = (int)next_t;
+    __syncthreads();  // every wave has read next_t before thread 0 rewrites it (an empty expert's
+                      // iteration has no barrier of its own)
     int pg = -1, pct = 0, pr0 = 0, pr1 = 0;  // the deferred tile
     while (t < count) {
         // draw the next ticket now; its result is needed only after this tile

@@ -92,6 +92,28 @@ def test_exchange_timeout_fixup(cb, orc, overrides, counts, K, N):
     assert gave_up in (0, 1)
 
 
+def test_decode_exchange_waits_for_every_lane(cb, orc):
+    """Every row of a 16-row block must wait for all of its column tiles' maxima, the rows held by
+    lanes 32-63 of a wave (block positions 8-15) included: a wait that decided on the lower 32
+    lanes only let those rows requantise with a partial maximum now and then.  Eight calls in a
+    row agree bit for bit and match the oracle."""
+    counts, K, N = [5, 0, 17, 32, 1, 9] * 8, 448, 4096
+    x, w, ws, xs, gl = _inputs(counts, K, N, 9001)
+    yr, ysr = orc.gmsq(x.cpu().numpy(), w.cpu().numpy(), ws.cpu().numpy(), xs.cpu().numpy(), np.array(gl))
+    first = None
+    for i in range(8):
+        y, ys, _ = _run_raw(cb, x, w, ws, xs, gl)
+        torch.cuda.synchronize()
+        y, ys = y.cpu().numpy(), ys.cpu().numpy()
+        if first is None:
+            first = (y, ys)
+            np.testing.assert_allclose(ys, ysr, rtol=1e-5)
+            assert np.abs(y.astype(np.int32) - yr.astype(np.int32)).max() <= 1
+        else:
+            np.testing.assert_array_equal(y, first[0], err_msg=f"call {i}")
+            np.testing.assert_array_equal(ys, first[1], err_msg=f"call {i}")
+
+
 def test_int32_core_tile_bytes_past_4gib(cb):
     """E = 1, M = 131072, N = 8192: the first tile's rows x row bytes to the group end are 2^32 bytes
     of int32 output (and 131072 x 256 bytes of activations); every tile must still be written."""
