@@ -26,6 +26,7 @@ CB_ERR_WORKSPACE = 12
 CB_ERR_EMPTY = 13
 CB_ERR_LAUNCH = 14
 CB_ERR_NO_DEVICE = 15
+CB_ERR_SCRATCH_LIMIT = 16
 
 # dtype codes (cb_dtype)
 CB_DT_FLOAT16 = 1
@@ -56,6 +57,7 @@ SIGNATURES = {
     "cb_grouped_matmul_swiglu_quant": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P]),
     "cb_grouped_matmul_swiglu_quant_status": (_I, [_P, _I64, _I64, _I64, _P, _P]),
     "cb_set_test_overrides": (None, [_I, _I, _I]),
+    "cb_grouped_matmul_swiglu_quant_noalloc": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "cb_grouped_matmul_swiglu_quant_gather": (_I, [_P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _P]),
     "cb_quant_matmul": (_I, [_P, _P, _P, _I, _I64, _P, _I64, _P, _I64, _P, _I, _I64, _I, _I64, _I64, _I64, _I64, _I, _P, _P]),
     "cb_grouped_matmul_quant": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P]),

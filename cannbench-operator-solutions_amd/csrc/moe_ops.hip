@@ -190,6 +190,7 @@ extern "C" const char* cb_status_string(int s)
         case CB_ERR_EMPTY: return "non-empty shapes required";
         case CB_ERR_LAUNCH: return "HIP kernel launch failed";
         case CB_ERR_NO_DEVICE: return "no usable gfx950 device";
+        case CB_ERR_SCRATCH_LIMIT: return "problem exceeds the fixed scratch of the no-allocation entry point";
         default: return "unknown status";
     }
 }
@@ -342,6 +343,53 @@ extern "C" int cb_grouped_matmul_swiglu_quant_gather(const int8_t* x, int64_t x_
     if (!row_index && M > 0 && N > 0 && E > 0) return CB_ERR_NULL_POINTER;
     return gmsq_impl(x, x_rows, row_index, weight, weight_scale, x_scale, group_list, group_len, M, K, N, E, y,
                      y_scale, workspace, workspace_bytes, stream);
+}
+
+// The fixed workspace of cb_grouped_matmul_swiglu_quant_noalloc: one array per GPU (each device
+// holds its own copy of a __device__ variable).  Host code uses the address looked up on each
+// device, never the array's name.
+static constexpr int64_t kNoAllocScratchBytes = 4 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+// Device address of `scratch` on the current device, looked up once per device.
+static void* noalloc_scratch(int* status)
+{
+    static std::mutex mu;
+    static void* ptrs[64] = {nullptr};
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        *status = CB_ERR_NO_DEVICE;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptrs[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+            *status = CB_ERR_NO_DEVICE;
+            return nullptr;
+        }
+        ptrs[dev] = p;
+    }
+    *status = CB_OK;
+    return ptrs[dev];
+}
+
+extern "C" int cb_grouped_matmul_swiglu_quant_noalloc(const int8_t* x, const int8_t* weight,
+                                                      const float* weight_scale, const float* x_scale,
+                                                      const int64_t* group_list, int64_t group_len, int64_t M,
+                                                      int64_t K, int64_t N, int64_t E, int8_t* y, float* y_scale,
+                                                      void* stream)
+{
+    // the checks that come before any workspace use, in the order of the workspace entry point
+    if (M < 0 || K < 0 || N < 0 || E < 0) return CB_ERR_SHAPE;
+    if (N % 2 != 0) return CB_ERR_N_ODD;
+    if (M == 0 || N == 0 || E == 0) return CB_OK;
+    if (gmsq_workspace(M, N, E).total > kNoAllocScratchBytes) return CB_ERR_SCRATCH_LIMIT;
+    int rc = CB_OK;
+    void* ws = noalloc_scratch(&rc);
+    if (rc != CB_OK) return rc;
+    return gmsq_impl(x, M, nullptr, weight, weight_scale, x_scale, group_list, group_len, M, K, N, E, y, y_scale, ws,
+                     kNoAllocScratchBytes, stream);
 }
 
 extern "C" int cb_grouped_matmul_swiglu_quant_status(const void* workspace, int64_t M, int64_t N, int64_t E,

@@ -46,7 +46,8 @@ typedef enum cb_status {
     CB_ERR_WORKSPACE = 12,         /* workspace missing or smaller than *_workspace_size()    */
     CB_ERR_EMPTY = 13,             /* QuantMatmul requires non-empty M, K, N                 */
     CB_ERR_LAUNCH = 14,            /* the HIP runtime refused a launch                       */
-    CB_ERR_NO_DEVICE = 15          /* no usable gfx950 device                                */
+    CB_ERR_NO_DEVICE = 15,         /* no usable gfx950 device                                */
+    CB_ERR_SCRATCH_LIMIT = 16      /* beyond the fixed scratch of a no-allocation entry point */
 } cb_status;
 
 /* dtype codes for the typed arguments. */
@@ -166,6 +167,23 @@ int cb_grouped_matmul_swiglu_quant_gather(const int8_t* x, int64_t x_rows, const
  */
 int cb_grouped_matmul_swiglu_quant_status(const void* workspace, int64_t M, int64_t N, int64_t E,
                                           uint32_t* status, void* stream);
+
+/*
+ * GroupedMatmulSwigluQuant without a workspace argument and without any allocation.
+ * No reference counterpart: for callers that cannot allocate device memory or pass a workspace
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, validation, results and stream behaviour as cb_grouped_matmul_swiglu_quant, with the
+ * workspace taken from a fixed 4 MiB device array of the library (one per GPU, held until the
+ * process ends; its address is looked up once per device on the first call there).  Problems whose
+ * workspace would exceed 4 MiB return CB_ERR_SCRATCH_LIMIT (M = 131072 rows with N = 4096 and
+ * E = 256 need about 0.7 MiB; the limit is reached near M = 979000).  Every call on one GPU shares
+ * that GPU's array: calls that may overlap on one device (different streams, threads or
+ * processes) race and must be ordered by the caller.
+ */
+int cb_grouped_matmul_swiglu_quant_noalloc(const int8_t* x, const int8_t* weight, const float* weight_scale,
+                                           const float* x_scale, const int64_t* group_list, int64_t group_len,
+                                           int64_t M, int64_t K, int64_t N, int64_t E, int8_t* y,
+                                           float* y_scale, void* stream);
 
 /*
  * Test hook (no reference counterpart; for this library's tests only).  Overrides for the calling
