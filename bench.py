@@ -350,17 +350,26 @@ def bench_copy(steps, warmup, dev):
     return {"ms": ms, "gbs": 2 * n / (ms * 1e-3) / 1e9, "bytes_read": n, "bytes_written": n}
 
 
-def traffic_from_profiles(kernel_tag):
+def traffic_from_profiles(kernel_tag, kernel):
     """HBM bytes per launch of a kernel as recorded in profiles/<kernel_tag>_traffic.md (a line
     'traffic_bytes_per_launch: N', derived from FETCH_SIZE + WRITE_SIZE scaled by the copy-kernel
-    calibration), or None when no such summary is committed."""
+    calibration), or None when no such summary is committed or when the summary's 'kernel_name:'
+    line does not name `kernel` (the kernel this library launches today), so that a figure measured
+    on an earlier kernel is never reported."""
     path = os.path.join(ROOT, "profiles", f"{kernel_tag}_traffic.md")
     if not os.path.exists(path):
         return None
+    name, value = None, None
     for line in open(path):
-        if line.strip().startswith("traffic_bytes_per_launch:"):
-            return int(float(line.split(":", 1)[1].strip()))
-    return None
+        line = line.strip()
+        if line.startswith("kernel_name:"):
+            name = line.split(":", 1)[1].strip()
+        elif line.startswith("traffic_bytes_per_launch:"):
+            value = int(float(line.split(":", 1)[1].strip()))
+    return value if name is not None and kernel in name else None
+
+
+ROUTING_KERNELS = {"finalize": "cb::mfr_vec_kernel", "rerouting": "cb::mrr_copy_kernel", "dqsq": "cb::dqsq_vec_kernel"}
 
 
 def cpu_baseline(d, budget_s=12.0):
@@ -388,7 +397,10 @@ def cpu_baseline(d, budget_s=12.0):
         if t_total >= budget_s:
             break
     ops = 2.0 * done_rows * K * N
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    # OpenMP runs one thread per core of this process's CPU set unless OMP_NUM_THREADS says fewer
+    cores = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        cores = min(cores, int(os.environ["OMP_NUM_THREADS"]))
     return {"value": round(ops / t_total / 1e12, 4), "unit": "TOPS", "cores": cores, "kind": "port",
             "sample": f"oracle/cb_oracle.c or_gmsq (OpenMP) on {done_rows} rows = {len(experts)} whole experts "
                       f"of the prefill config, {t_total:.1f} s"}
@@ -458,13 +470,13 @@ def main():
         out["copy"] = {"value": round(c["gbs"], 1), "unit": "GB/s", "ms_per_step": round(c["ms"], 4),
                        "bytes_read": c["bytes_read"], "bytes_written": c["bytes_written"]}
     if out.get("roofline") is not None:
-        out["roofline"]["traffic"] = traffic_from_profiles("prefill_gemm")
+        out["roofline"]["traffic"] = traffic_from_profiles("prefill_gemm", "cb::gmsq_prefill_kernel(")
     if "decode" in out:
-        out["decode"]["roofline"]["traffic"] = traffic_from_profiles("decode_gemm")
-        out["down_proj"]["roofline"]["traffic"] = traffic_from_profiles("down_proj_gemm")
+        out["decode"]["roofline"]["traffic"] = traffic_from_profiles("decode_gemm", "cb::gmsq_decode_kernel(")
+        out["down_proj"]["roofline"]["traffic"] = traffic_from_profiles("down_proj_gemm", "cb::skinny_kernel<1")
     for name in ("finalize", "rerouting", "dqsq"):
         if name in out.get("routing", {}):
-            out["routing"][name]["roofline"]["traffic"] = traffic_from_profiles("routing_" + name)
+            out["routing"][name]["roofline"]["traffic"] = traffic_from_profiles("routing_" + name, ROUTING_KERNELS[name])
     if not args.no_cpu and "prefill" in keep:
         out["cpu_baseline"] = cpu_baseline(keep["prefill"])
     print(json.dumps(out), flush=True)
