@@ -287,6 +287,9 @@ __global__ __launch_bounds__(256, 2) void gmsq_decode_kernel(const GemmArgs a, c
 __global__ __launch_bounds__(256, 2) void gmsq_decode_fixup_kernel(const GemmArgs a)
 {
     __shared__ int red[3][4][16][64];
+    // no wait timed out in the main launch (status word 0): nothing is marked
+    if (__builtin_amdgcn_readfirstlane(__hip_atomic_load(a.epi.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == 0)
+        return;
     const int total = a.gt.n_groups * a.ntiles;
     for (int t = blockIdx.x; t < total; t += gridDim.x) {
         if (__builtin_amdgcn_readfirstlane(__hip_atomic_load(a.epi.redo + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == 0)

@@ -17,18 +17,19 @@
 //   iteration kt, half 1 (MFMAs of step 0): the B chunks of stage kt + 3
 //   barrier (stage kt + 1 has landed; every wave has finished reading stage kt)
 //   iteration kt, half 2 (MFMAs of step 1): the A chunks of stage kt + 4 into stage kt's slot
-// so 2.5 stages (80 KB) are in flight while one is multiplied.  Stages past K fetch nothing.
+// so 2.5 stages (80 KB) are in flight while one is multiplied.  The stream runs on across tiles:
+// the stages past K are the workgroup's next tile's first 3.5 stages (its prologue), issued while
+// the last stages of this tile are multiplied, so they arrive during this tile's epilogue and no
+// tile starts with a burst of DMAs.  Stage kt of a tile lives in ring slot (rb + kt) % 4.
 //
-// Epilogue, per tile:
-//   1. wait for every DMA (the dead ones past K), barrier: the ring is free;
-//   2. issue the next tile's first 3.5 stages and fetch its scales, so their latency hides under
-//      steps 3-6;
-//   3. SwiGLU from the accumulators (the reference's operation order), |act| row maxima reduced
+// Epilogue, per tile (it does not touch the ring; the tile's scales sit in one of two LDS slots,
+// written during the previous tile's epilogue):
+//   1. SwiGLU from the accumulators (the reference's operation order), |act| row maxima reduced
 //      across lanes (DPP) and across the two waves sharing rows (LDS), one device-scope atomicMax
 //      per (row, tile);
-//   4. arrival count for the round's exchange group, then a bounded wait until every column tile
+//   2. arrival count for the round's exchange group, then a bounded wait until every column tile
 //      of the group's row tiles has published;
-//   5. per-row 127 / amax through LDS, rint16 in registers, a 4 x 4 byte transpose across each
+//   3. per-row 127 / amax through LDS, rint16 in registers, a 4 x 4 byte transpose across each
 //      lane quad, and dword stores of int8 y (four consecutive columns per lane).
 // A column tile whose wait times out marks itself in the workspace and stores nothing; the fix-up
 // launch that always follows recomputes exactly those tiles with the final row maxima, so the
@@ -41,13 +42,102 @@ namespace cb {
 
 
 using PfCfg = LdsCfg<2, 2, 4, 64>;
-using PfDma = TileDma<PfCfg, true>;
 
-// LDS map (bytes): the ring, then per-row activation scales [256], per-column weight scales
-// [256] (128 gate then 128 up), row maxima of the two column-half waves [2][256], 127 / amax [256],
-// the round-order table.
+// DMA plan.  A lane's chunk offsets within a stage depend only on the workgroup's column tile
+// (fixed for the launch) and, for contiguous rows, not on the row tile at all: PfOffs holds them
+// once per workgroup, and a tile contributes only its two buffer resources (PfSrc; rows past the
+// tile's valid rows lie outside the activation resource and read zeros).  Gathered rows (GATHER)
+// add per-tile source-row offsets.
+struct PfOffs {
+    uint32_t a[4], b[4];
+    uint32_t n;  // weight row length
+};
+struct PfSrc {
+    __amdgpu_buffer_rsrc_t ares, bres;
+    uint32_t ga[4];  // GATHER: source row * K of each A chunk (0x80000000: no row)
+};
+
+template <bool GATHER>
+__device__ __forceinline__ PfOffs pf_offsets(const GemmArgs& a, const int nt, const int wave, const int lane)
+{
+    PfOffs o;
+    const uint32_t K = (uint32_t)a.K;
+    o.n = (uint32_t)a.N;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int cid = (i * 4 + wave) * 64 + lane;  // 16-byte chunk id in the A tile
+        const int row = cid >> 2, pos = cid & 3;
+        const uint32_t q16 = (uint32_t)((pos ^ a_swizzle<4>(row)) * 16);
+        o.a[i] = GATHER ? q16 : (uint32_t)row * K + q16;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int cid = (i * 4 + wave) * 64 + lane;
+        const int row = cid >> 4, pos = cid & 15;
+        const int c = pos ^ ((row & 7) << 1);  // logical 16-column chunk: gate (c < 8) or up
+        const int64_t j = (int64_t)nt * 128 + 16 * (c & 7);
+        const int64_t col = c < 8 ? j : a.epi.H + j;
+        o.b[i] = (uint32_t)row * o.n + (uint32_t)(j < a.epi.H ? col : 0);
+    }
+    return o;
+}
+
+template <bool GATHER>
+__device__ __forceinline__ PfSrc pf_src(const GemmArgs& a, const int g, const int m0, const int vrows, const int wave,
+                                        const int lane)
+{
+    PfSrc s;
+    const int64_t K = a.K;
+    s.ares = GATHER ? make_rsrc(a.x, (uint32_t)(a.x_rows * K))
+                    : make_rsrc(a.x + (int64_t)m0 * K, (uint32_t)((int64_t)(vrows < 256 ? vrows : 256) * K));
+    s.bres = make_rsrc(a.w + (int64_t)g * a.w_gstride, (uint32_t)(K * a.N));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        s.ga[i] = 0x80000000u;
+        if constexpr (GATHER) {
+            const int row = ((i * 4 + wave) * 64 + lane) >> 2;
+            const int srow = row < vrows ? src_row(a, m0 + row) : -1;
+            if (srow >= 0) s.ga[i] = (uint32_t)srow * (uint32_t)K;
+        }
+    }
+    return s;
+}
+
+// A plan that fetches nothing: the stage stream past a workgroup's last tile.
+__device__ __forceinline__ PfSrc pf_dead(const GemmArgs& a)
+{
+    PfSrc s;
+    s.ares = make_rsrc(a.x, 0u);
+    s.bres = make_rsrc(a.w, 0u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s.ga[i] = 0x80000000u;
+    return s;
+}
+
+// DMA chunk I of stage kt into ring slot `slot` (I < 4: activation chunk I, else weight chunk
+// I - 4).  CHECK: stages past K fetch nothing (activation offsets would run into the next rows;
+// weight offsets already lie outside their resource).
+template <int I, bool GATHER, bool CHECK>
+__device__ __forceinline__ void pf_dma(const PfSrc& s, const PfOffs& o, const int kt, const int nk, const int slot,
+                                       const uint32_t lds_base, const int wave)
+{
+    using C = PfCfg;
+    const uint32_t sa = lds_base + (uint32_t)(slot * C::STAGE);
+    if constexpr (I < 4) {
+        uint32_t off = (GATHER ? s.ga[I] + o.a[I] : o.a[I]) + (uint32_t)(kt * C::BK);
+        if (CHECK && kt >= nk) off = 0x80000000u;
+        dma16(s.ares, off, __builtin_amdgcn_readfirstlane(sa + (uint32_t)((I * 4 + wave) * 1024)));
+    } else {
+        dma16(s.bres, o.b[I - 4] + (uint32_t)(kt * C::BK) * o.n,
+              __builtin_amdgcn_readfirstlane(sa + C::A_BYTES + (uint32_t)(((I - 4) * 4 + wave) * 1024)));
+    }
+}
+
+// LDS map (bytes): the ring, then two scale slots (alternate tiles), each the per-row activation
+// scales [256] and per-column weight scales [256] (128 gate then 128 up), row maxima of the two
+// column-half waves [2][256], 127 / amax [256], the round-order table.
 constexpr int kPfRing = PfCfg::STAGES_ * PfCfg::STAGE;
-constexpr int kPfXs = kPfRing, kPfCs = kPfXs + 1024, kPfRm = kPfCs + 1024, kPfInv = kPfRm + 2048;
+constexpr int kPfSc = kPfRing, kPfScSlot = 2048, kPfRm = kPfSc + 2 * kPfScSlot, kPfInv = kPfRm + 2048;
 constexpr int kPfOrd = kPfInv + 1024;
 constexpr int kPfLds = kPfOrd + 3 * 4 * (CB_MAX_EXPERTS + 1);
 static_assert(PfCfg::A_ISSUE == 4 && PfCfg::B_ISSUE == 4 && PfCfg::NW == 4 && PfCfg::FM == 4 && PfCfg::FN == 4,
@@ -195,27 +285,50 @@ __device__ __forceinline__ PfTile pf_tile_at(const GroupTable& gt, int mt)
 __device__ __forceinline__ int pf_total_rounds(const PfOrder& o) { return o.heavy_rounds + o.light_rounds; }
 
 // ---- the K loop ------------------------------------------------------------------------------
-// Ring slot of stage kt: kt % 4 (every tile starts its stage count at slot 0).
-template <int NV>
-__device__ __forceinline__ void pf_kloop(const PfDma& dma, uint8_t* smem, const uint32_t (&a_rd)[4][2],
-                                         const uint32_t (&b_rd)[4], v16i (&acc)[4][4], const int wave,
-                                         const bool first)
+// The plan of stage st of the stream: this tile's, or past K (PF) the next tile's (stage st - nk).
+// Value selects, not control flow, so the scheduled loop body stays one block.
+template <bool PF>
+__device__ __forceinline__ PfSrc pf_stream(const PfSrc& cur, const PfSrc& nxt, const int st, const int nk, int& lst)
+{
+    if constexpr (!PF) {
+        lst = st;
+        return cur;
+    } else {
+        const bool n = st >= nk;
+        lst = n ? st - nk : st;
+        PfSrc s;
+        s.ares = n ? nxt.ares : cur.ares;
+        s.bres = n ? nxt.bres : cur.bres;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s.ga[i] = n ? nxt.ga[i] : cur.ga[i];
+        return s;
+    }
+}
+
+// Ring slot of stage kt: (rb + kt) % 4.  With PF (nk >= 4) the stages past this tile's K are the
+// next tile's first 3.5 stages (its prologue), so the next tile starts at ring slot (rb + nk) % 4
+// with its stages already in flight; nxt is a dead plan when there is no next tile.  Without PF
+// they fetch nothing.
+template <int NV, bool PF, bool GATHER>
+__device__ __forceinline__ void pf_kloop(const PfSrc& dma, const PfSrc& nxt, const PfOffs& offs, const int nk,
+                                         const int rb, uint8_t* smem,
+                                         const uint32_t (&a_rd)[4][2], const uint32_t (&b_rd)[4], v16i (&acc)[4][4],
+                                         const int wave, const bool first)
 {
     using C = PfCfg;
     constexpr int NVA = NV > 0 ? NV : 1;
     const uint32_t lds_base = (uint32_t)(uintptr_t)(CB_LDS uint8_t*)smem;
     const CB_LDS uint8_t* sm = (const CB_LDS uint8_t*)smem;
-    const int nk = __builtin_amdgcn_readfirstlane(dma.nk);
     v4i a0[NVA], a1[NVA], b0[4], b1[4];
     auto rdb = [&](int kt, int ks, int fn, v4i (&bf)[4]) {
-        const CB_LDS uint8_t* base = sm + (kt & 3) * C::STAGE + C::A_BYTES;
+        const CB_LDS uint8_t* base = sm + ((rb + kt) & 3) * C::STAGE + C::A_BYTES;
         const uint32_t o = b_rd[fn] + (uint32_t)(ks * 32 * C::BN);
         const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((CB_LDS v2i*)(base + o));
         const v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32((CB_LDS v2i*)(base + o + 8 * C::BN));
         bf[fn] = v4i{lo[0], lo[1], hi[0], hi[1]};
     };
     auto rda = [&](int kt, int ks, int fm, v4i (&af)[NVA]) {
-        if (fm < NV) af[fm < NVA ? fm : 0] = *(const CB_LDS v4i*)(sm + (kt & 3) * C::STAGE + a_rd[fm][ks]);
+        if (fm < NV) af[fm < NVA ? fm : 0] = *(const CB_LDS v4i*)(sm + ((rb + kt) & 3) * C::STAGE + a_rd[fm][ks]);
     };
     auto mrow = [&](int fm, const v4i (&af)[NVA], const v4i (&bf)[4]) {
         if (fm < NV) {
@@ -237,7 +350,8 @@ __device__ __forceinline__ void pf_kloop(const PfDma& dma, uint8_t* smem, const 
         __builtin_amdgcn_sched_barrier(0);
     };
     // stage 0 landed: the first tile of a workgroup waits for its DMAs; a later tile's prologue was
-    // drained by its predecessor's epilogue (every VMEM result waited for), so only the barrier
+    // drained by its predecessor's epilogue (every VMEM result waited for before its exchange), so
+    // only the barrier
     if (first) wait_vmcnt_barrier<2 * C::ISSUE + C::A_ISSUE>();
     else wait_vmcnt_barrier<63>();
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0) in the compiler's own accounting
@@ -247,23 +361,27 @@ __device__ __forceinline__ void pf_kloop(const PfDma& dma, uint8_t* smem, const 
 #pragma unroll
         for (int c = 0; c < 4; ++c) rda(0, 0, c, a0);
     }
+#pragma nounroll
     for (int kt = 0; kt < nk; ++kt) {
+        int sb, sa;
+        const PfSrc db = pf_stream<PF>(dma, nxt, kt + 3, nk, sb);
+        const PfSrc da = pf_stream<PF>(dma, nxt, kt + 4, nk, sa);
         // half 1: MFMAs of step 0 (a0/b0), reads of step 1, the B chunks of stage kt + 3
-        const int s3 = (kt + 3) & 3;
-        dma.template issue_one<4>(kt + 3, s3, lds_base, wave);
+        const int s3 = (rb + kt + 3) & 3;
+        pf_dma<4, GATHER, !PF>(db, offs, sb, nk, s3, lds_base, wave);
         if constexpr (NV > 0) { rdb(kt, 1, 0, b1); rdb(kt, 1, 1, b1); }
         mrow(0, a0, b0);
         fence();
-        dma.template issue_one<5>(kt + 3, s3, lds_base, wave);
+        pf_dma<5, GATHER, !PF>(db, offs, sb, nk, s3, lds_base, wave);
         if constexpr (NV > 0) { rdb(kt, 1, 2, b1); rdb(kt, 1, 3, b1); }
         mrow(1, a0, b0);
         fence();
-        dma.template issue_one<6>(kt + 3, s3, lds_base, wave);
+        pf_dma<6, GATHER, !PF>(db, offs, sb, nk, s3, lds_base, wave);
         rda(kt, 1, 0, a1);
         rda(kt, 1, 1, a1);
         mrow(2, a0, b0);
         fence();
-        dma.template issue_one<7>(kt + 3, s3, lds_base, wave);
+        pf_dma<7, GATHER, !PF>(db, offs, sb, nk, s3, lds_base, wave);
         rda(kt, 1, 2, a1);
         rda(kt, 1, 3, a1);
         mrow(3, a0, b0);
@@ -272,21 +390,21 @@ __device__ __forceinline__ void pf_kloop(const PfDma& dma, uint8_t* smem, const 
         wait_vmcnt_barrier<2 * C::ISSUE>();
         // half 2: MFMAs of step 1 (a1/b1), reads of stage kt + 1 step 0, the A chunks of stage
         // kt + 4 into the slot stage kt just left
-        const int s4 = kt & 3;
-        dma.template issue_one<0>(kt + 4, s4, lds_base, wave);
+        const int s4 = (rb + kt) & 3;
+        pf_dma<0, GATHER, !PF>(da, offs, sa, nk, s4, lds_base, wave);
         if constexpr (NV > 0) { rdb(kt + 1, 0, 0, b0); rdb(kt + 1, 0, 1, b0); }
         mrow(0, a1, b1);
         fence();
-        dma.template issue_one<1>(kt + 4, s4, lds_base, wave);
+        pf_dma<1, GATHER, !PF>(da, offs, sa, nk, s4, lds_base, wave);
         if constexpr (NV > 0) { rdb(kt + 1, 0, 2, b0); rdb(kt + 1, 0, 3, b0); }
         mrow(1, a1, b1);
         fence();
-        dma.template issue_one<2>(kt + 4, s4, lds_base, wave);
+        pf_dma<2, GATHER, !PF>(da, offs, sa, nk, s4, lds_base, wave);
         rda(kt + 1, 0, 0, a0);
         rda(kt + 1, 0, 1, a0);
         mrow(2, a1, b1);
         fence();
-        dma.template issue_one<3>(kt + 4, s4, lds_base, wave);
+        pf_dma<3, GATHER, !PF>(da, offs, sa, nk, s4, lds_base, wave);
         rda(kt + 1, 0, 2, a0);
         rda(kt + 1, 0, 3, a0);
         mrow(3, a1, b1);
@@ -295,15 +413,26 @@ __device__ __forceinline__ void pf_kloop(const PfDma& dma, uint8_t* smem, const 
 }
 
 // Prologue of a tile: stages 0-2 and the A chunks of stage 3 (the loop issues the rest).
-__device__ __forceinline__ void pf_prologue(const PfDma& dma, uint8_t* smem, const int wave)
+template <bool GATHER>
+__device__ __forceinline__ void pf_prologue(const PfSrc& s, const PfOffs& o, const int nk, uint8_t* smem,
+                                            const int wave)
 {
     const uint32_t lds_base = (uint32_t)(uintptr_t)(CB_LDS uint8_t*)smem;
 #pragma unroll
-    for (int st = 0; st < 3; ++st) dma.issue_at(st, st, lds_base, wave);
-    dma.template issue_one<0>(3, 3, lds_base, wave);
-    dma.template issue_one<1>(3, 3, lds_base, wave);
-    dma.template issue_one<2>(3, 3, lds_base, wave);
-    dma.template issue_one<3>(3, 3, lds_base, wave);
+    for (int st = 0; st < 3; ++st) {
+        pf_dma<0, GATHER, true>(s, o, st, nk, st, lds_base, wave);
+        pf_dma<1, GATHER, true>(s, o, st, nk, st, lds_base, wave);
+        pf_dma<2, GATHER, true>(s, o, st, nk, st, lds_base, wave);
+        pf_dma<3, GATHER, true>(s, o, st, nk, st, lds_base, wave);
+        pf_dma<4, GATHER, true>(s, o, st, nk, st, lds_base, wave);
+        pf_dma<5, GATHER, true>(s, o, st, nk, st, lds_base, wave);
+        pf_dma<6, GATHER, true>(s, o, st, nk, st, lds_base, wave);
+        pf_dma<7, GATHER, true>(s, o, st, nk, st, lds_base, wave);
+    }
+    pf_dma<0, GATHER, true>(s, o, 3, nk, 3, lds_base, wave);
+    pf_dma<1, GATHER, true>(s, o, 3, nk, 3, lds_base, wave);
+    pf_dma<2, GATHER, true>(s, o, 3, nk, 3, lds_base, wave);
+    pf_dma<3, GATHER, true>(s, o, 3, nk, 3, lds_base, wave);
 }
 
 // Scales of a tile, fetched into registers: thread t takes tile row t's activation scale (the row
@@ -406,9 +535,8 @@ __device__ __forceinline__ int rint16_h(float v)
 // fix-up launch).
 template <bool FIXUP>
 __device__ __forceinline__ void pf_epilogue(const GemmArgs& a, uint8_t* smem, v16i (&acc)[4][4], const PfTile& t,
-                                            const int nt, const PfScales& sc, const int arr_idx,
-                                            const u32 arr_target, const int tile_id, const PfDma& nxt,
-                                            const bool has_nxt)
+                                            const int nt, const int par, const int arr_idx, const u32 arr_target,
+                                            const int tile_id)
 {
     // opaque: the per-tile address math is recomputed here rather than hoisted out of the tile loop
     // (and spilled across the K loop)
@@ -418,20 +546,14 @@ __device__ __forceinline__ void pf_epilogue(const GemmArgs& a, uint8_t* smem, v1
     const EpiArgs& e = a.epi;
     const int64_t H = e.H;
     const int m0 = t.m0, vrows = t.vrows;
-    CB_LDS float* xs_l = (CB_LDS float*)((CB_LDS uint8_t*)smem + kPfXs);
-    CB_LDS float* cs_l = (CB_LDS float*)((CB_LDS uint8_t*)smem + kPfCs);
+    const CB_LDS float* xs_l = (const CB_LDS float*)((CB_LDS uint8_t*)smem + kPfSc + par * kPfScSlot);
+    const CB_LDS float* cs_l = xs_l + 256;
     CB_LDS float* rm_l = (CB_LDS float*)((CB_LDS uint8_t*)smem + kPfRm);
     CB_LDS float* inv_l = (CB_LDS float*)((CB_LDS uint8_t*)smem + kPfInv);
 
-    // 1. every DMA of this tile (the dead ones past K included) has landed and every wave has
-    //    finished its ring reads; the scales of this tile go to LDS
-    xs_l[tid] = sc.xs;
-    cs_l[tid] = sc.cs;
-    epi_barrier();
-    // 2. the next tile's prologue (its plan and scales were prepared before this tile's K loop)
-    if (!FIXUP && has_nxt) pf_prologue(nxt, smem, wave);
-
-    // 3. SwiGLU.  Lane (h = lane / 32, c = lane % 32) of fragment (fm, fn) holds rows
+    // Nothing to wait for first: the ring's slots already take the next tile's first stages, and
+    // this tile's scales are in LDS slot par since before its K loop.
+    // 1. SwiGLU.  Lane (h = lane / 32, c = lane % 32) of fragment (fm, fn) holds rows
     //    (2 fm + wm) * 32 + 8 (r / 4) + 4 h + r % 4 (r = 0..15), column c of the fragment.
     const int h = lane >> 5, c = lane & 31;
     float wsg[2], wsu[2];
@@ -508,7 +630,7 @@ __device__ __forceinline__ void pf_epilogue(const GemmArgs& a, uint8_t* smem, v1
             const u32 m0v = __float_as_uint(rm_l[tid]), m1v = __float_as_uint(rm_l[256 + tid]);
             __hip_atomic_fetch_max(e.amax + m0 + tid, m0v > m1v ? m0v : m1v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        // 4. exchange: every row maximum of this tile has completed before the arrival count
+        // 2. exchange: every row maximum of this tile has completed before the arrival count
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (tid == 0) {
@@ -537,15 +659,15 @@ __device__ __forceinline__ void pf_epilogue(const GemmArgs& a, uint8_t* smem, v1
         }
     }
 
-    // 5. final row maxima -> 127 / amax through LDS; the nt = 0 tile writes y_scale
+    // 3. final row maxima -> 127 / amax through LDS; the nt = 0 tile writes y_scale
     {
         float am = 0.0f;
         if (tid < vrows) am = __uint_as_float(__hip_atomic_load(e.amax + m0 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
         if (!(am > kFltMin)) am = kFltMin;
         inv_l[tid] = 127.0f / am;
         if (nt == 0 && tid < vrows) e.yq_scale[m0 + tid] = am * kInv127;
-        // every VMEM result (the next tile's prologue included) is in before the stores below, so
-        // the next tile's loop starts without a vmcnt wait
+        // every VMEM result (the next tile's first stages included) is in before the stores below,
+        // so the next tile's loop starts without a vmcnt wait
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     }
@@ -581,7 +703,9 @@ __device__ __forceinline__ void pf_epilogue(const GemmArgs& a, uint8_t* smem, v1
 
 // Persistent GroupedMatmulSwigluQuant prefill kernel.  gridDim.x workgroups, at most one per CU,
 // all resident together (the host checks the occupancy).  Exchange group q = round q of slot s:
-// its RT row tiles x ntl column tiles meet at arrive[q] once per round.
+// its RT row tiles x ntl column tiles meet at arrive[q] once per round.  GATHER: activation rows
+// through the row index.
+template <bool GATHER>
 __global__ __launch_bounds__(256, 1) void gmsq_prefill_kernel(const GemmArgs a)
 {
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
@@ -596,21 +720,32 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_kernel(const GemmArgs a)
     const u32 target = (u32)(pl.RT * ntl);
     uint32_t a_rd[4][2], b_rd[4];
     pf_read_offsets(wm, wn, lane, a_rd, b_rd);
+    const int nk = __builtin_amdgcn_readfirstlane((int)((a.K + PfCfg::BK - 1) / PfCfg::BK));
+    const PfOffs offs = pf_offsets<GATHER>(a, pl.nt, wave, lane);
 
     int q = pl.slot;
     if (q >= rounds) return;
+    // this tile's scales into LDS slot par (the wait for their loads also waits for the prologue)
+    auto put_scales = [&](const PfScales& v, int par) {
+        CB_LDS float* sl = (CB_LDS float*)((CB_LDS uint8_t*)smem + kPfSc + par * kPfScSlot);
+        sl[tid] = v.xs;
+        sl[256 + tid] = v.cs;
+    };
     PfTile cur_t = pf_round_tile(a.gt, tab, ord, pl.RT, q, pl.rt);
-    PfDma cur;
-    PfScales sc;
+    PfSrc cur;
+    int par = 0, rb = 0;  // scale slot and ring slot of the current tile
+    // the K loop carries the next tile's prologue when K spans at least 4 stages (the prologue's
+    // 3.5 stages then all lie in the last 4 iterations)
+    const bool pf = nk >= 4;
     if (cur_t.mt >= 0) {
-        cur.init_at(a, cur_t.g, cur_t.m0, cur_t.vrows, pl.nt, 0, wave, lane);
-        pf_prologue(cur, smem, wave);
-        sc = pf_scales(a, cur_t, pl.nt);
+        cur = pf_src<GATHER>(a, cur_t.g, cur_t.m0, cur_t.vrows, wave, lane);
+        pf_prologue<GATHER>(cur, offs, nk, smem, wave);
+        put_scales(pf_scales(a, cur_t, pl.nt), par);
     }
     bool first = true;
     for (; q < rounds; q += pl.slots) {
-        // the next round's tile of this workgroup: its plan and scales are prepared now, its
-        // prologue is issued by this tile's epilogue
+        // the next round's tile of this workgroup: its plan and scales are prepared now, and its
+        // first stages are fetched by this tile's K loop past K
         const int qn = q + pl.slots;
         const PfTile nxt_t = pf_round_tile(a.gt, tab, ord, pl.RT, qn, pl.rt);
         if (cur_t.mt < 0) {
@@ -618,19 +753,22 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_kernel(const GemmArgs a)
             if (tid == 0) __hip_atomic_fetch_add(a.epi.arrive + q, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (nxt_t.mt >= 0) {
                 __syncthreads();
-                cur.init_at(a, nxt_t.g, nxt_t.m0, nxt_t.vrows, pl.nt, 0, wave, opaque(lane));
-                pf_prologue(cur, smem, wave);
-                sc = pf_scales(a, nxt_t, pl.nt);
+                cur = pf_src<GATHER>(a, nxt_t.g, nxt_t.m0, nxt_t.vrows, wave, opaque(lane));
+                pf_prologue<GATHER>(cur, offs, nk, smem, wave);
+                put_scales(pf_scales(a, nxt_t, pl.nt), par);
+                rb = 0;
                 first = true;
             }
             cur_t = nxt_t;
             continue;
         }
-        PfDma nxt;
+        PfSrc nxt;
         PfScales nsc;
         if (nxt_t.mt >= 0) {
-            nxt.init_at(a, nxt_t.g, nxt_t.m0, nxt_t.vrows, pl.nt, 0, wave, opaque(lane));
+            nxt = pf_src<GATHER>(a, nxt_t.g, nxt_t.m0, nxt_t.vrows, wave, opaque(lane));
             nsc = pf_scales(a, nxt_t, pl.nt);
+        } else {
+            nxt = pf_dead(a);
         }
         v16i acc[4][4];
 #pragma unroll
@@ -642,33 +780,53 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_kernel(const GemmArgs a)
         // 32-row blocks with valid rows: wave row wm multiplies fragments fm with 2 fm + wm < nblk
         const int nblk = (cur_t.vrows + 31) / 32;
         const int nv = __builtin_amdgcn_readfirstlane(nblk > wm ? min((nblk - wm + 1) / 2, 4) : 0);
-        if (nv >= 4) pf_kloop<4>(cur, smem, a_rd, b_rd, acc, wave, first);
-        else if (nv == 3) pf_kloop<3>(cur, smem, a_rd, b_rd, acc, wave, first);
-        else if (nv == 2) pf_kloop<2>(cur, smem, a_rd, b_rd, acc, wave, first);
-        else if (nv == 1) pf_kloop<1>(cur, smem, a_rd, b_rd, acc, wave, first);
-        else pf_kloop<0>(cur, smem, a_rd, b_rd, acc, wave, first);
-        pf_epilogue<false>(a, smem, acc, cur_t, pl.nt, sc, q, target, cur_t.mt * ntl + pl.nt, nxt, nxt_t.mt >= 0);
-        // every wave is past its LDS reads of this epilogue before the next tile writes scales
-        __syncthreads();
-        if (nxt_t.mt >= 0) {
-            cur = nxt;
-            sc = nsc;
+        if (!first && !pf) {
+            // K below 4 stages: the previous loop could not carry this tile's prologue
+            pf_prologue<GATHER>(cur, offs, nk, smem, wave);
+            rb = 0;
+            first = true;
         }
+        if (pf) {
+            if (nv >= 4) pf_kloop<4, true, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+            else if (nv == 3) pf_kloop<3, true, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+            else if (nv == 2) pf_kloop<2, true, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+            else if (nv == 1) pf_kloop<1, true, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+            else pf_kloop<0, true, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+        } else {
+            if (nv >= 4) pf_kloop<4, false, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+            else if (nv == 3) pf_kloop<3, false, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+            else if (nv == 2) pf_kloop<2, false, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+            else if (nv == 1) pf_kloop<1, false, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+            else pf_kloop<0, false, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+        }
+        pf_epilogue<false>(a, smem, acc, cur_t, pl.nt, par, q, target, cur_t.mt * ntl + pl.nt);
+        if (nxt_t.mt >= 0) put_scales(nsc, par ^ 1);
+        // every wave is past its LDS reads of this epilogue (and the next scales are written)
+        // before the next tile's epilogue
+        __syncthreads();
+        rb = (rb + nk) & 3;
+        par ^= 1;
+        if (nxt_t.mt >= 0) cur = nxt;
         first = false;
         cur_t = nxt_t;
     }
 }
 
 // Fix-up launch: recomputes the tiles whose exchange wait timed out (redo[mt * ntl + nt] != 0),
-// now that every row maximum is final.  With nothing marked every workgroup exits after scanning.
+// now that every row maximum is final.  Without a timeout in the main launch (status word 0) every
+// workgroup exits at once.
+template <bool GATHER>
 __global__ __launch_bounds__(256, 1) void gmsq_prefill_fixup_kernel(const GemmArgs a)
 {
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    if (__builtin_amdgcn_readfirstlane(__hip_atomic_load(a.epi.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == 0)
+        return;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int ntl = a.ntiles;
     const int total = a.gt.total_mtiles * ntl;
+    const int nk = __builtin_amdgcn_readfirstlane((int)((a.K + PfCfg::BK - 1) / PfCfg::BK));
     uint32_t a_rd[4][2], b_rd[4];
     pf_read_offsets(wm, wn, lane, a_rd, b_rd);
     for (int t = blockIdx.x; t < total; t += gridDim.x) {
@@ -676,11 +834,16 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_fixup_kernel(const GemmAr
             continue;
         const int nt = t % ntl;
         const PfTile tl = pf_tile_at(a.gt, t / ntl);
-        PfDma cur;
-        cur.init_at(a, tl.g, tl.m0, tl.vrows, nt, 0, wave, opaque(lane));
+        const PfOffs offs = pf_offsets<GATHER>(a, nt, wave, opaque(lane));
+        const PfSrc cur = pf_src<GATHER>(a, tl.g, tl.m0, tl.vrows, wave, opaque(lane));
         __syncthreads();
-        pf_prologue(cur, smem, wave);
-        const PfScales sc = pf_scales(a, tl, nt);
+        pf_prologue<GATHER>(cur, offs, nk, smem, wave);
+        {
+            const PfScales sc = pf_scales(a, tl, nt);
+            CB_LDS float* sl = (CB_LDS float*)((CB_LDS uint8_t*)smem + kPfSc);
+            sl[tid] = sc.xs;
+            sl[256 + tid] = sc.cs;
+        }
         v16i acc[4][4];
 #pragma unroll
         for (int fm = 0; fm < 4; ++fm)
@@ -688,8 +851,8 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_fixup_kernel(const GemmAr
             for (int fn = 0; fn < 4; ++fn)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0;
-        pf_kloop<4>(cur, smem, a_rd, b_rd, acc, wave, true);
-        pf_epilogue<true>(a, smem, acc, tl, nt, sc, 0, 0, t, cur, false);
+        pf_kloop<4, false, GATHER>(cur, cur, offs, nk, 0, smem, a_rd, b_rd, acc, wave, true);
+        pf_epilogue<true>(a, smem, acc, tl, nt, 0, 0, 0, t);
         __syncthreads();
     }
 }

@@ -267,23 +267,27 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
         // prefill-shaped groups: the persistent GEMM with the requant fused
         const int cus = device_cus();
         const int grid = (ntl == 16 && cus >= 256) ? 256 : (cus / ntl) * ntl;
+        const bool gather = row_index != nullptr;
+        const void* main_k = gather ? (const void*)gmsq_prefill_kernel<true> : (const void*)gmsq_prefill_kernel<false>;
+        const void* fix_k =
+            gather ? (const void*)gmsq_prefill_fixup_kernel<true> : (const void*)gmsq_prefill_fixup_kernel<false>;
         int resident = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, (const void*)gmsq_prefill_kernel, 256, kPfLds) !=
-            hipSuccess)
-            resident = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, main_k, 256, kPfLds) != hipSuccess) resident = 0;
         // every workgroup of an exchange group must be resident at once: one per CU at most
         if (grid >= ntl && resident >= 1 && a.gt.total_mtiles + 2 <= ws.n_arrive) {
             a.ntiles = ntl;
             clear_ws((int64_t)a.gt.total_mtiles * ntl);
-            allow_dynamic_lds((const void*)gmsq_prefill_kernel, kPfLds);
-            allow_dynamic_lds((const void*)gmsq_prefill_fixup_kernel, kPfLds);
+            allow_dynamic_lds(main_k, kPfLds);
+            allow_dynamic_lds(fix_k, kPfLds);
+            const int tiles = a.gt.total_mtiles * ntl;
+            const dim3 fix_grid((unsigned)(tiles < 256 ? tiles : 256));
             {
                 TimedLaunch timed(st);
-                hipLaunchKernelGGL(gmsq_prefill_kernel, dim3((unsigned)grid), dim3(256), kPfLds, st, a);
+                if (gather) hipLaunchKernelGGL(gmsq_prefill_kernel<true>, dim3((unsigned)grid), dim3(256), kPfLds, st, a);
+                else hipLaunchKernelGGL(gmsq_prefill_kernel<false>, dim3((unsigned)grid), dim3(256), kPfLds, st, a);
             }
-            const int tiles = a.gt.total_mtiles * ntl;
-            hipLaunchKernelGGL(gmsq_prefill_fixup_kernel, dim3((unsigned)(tiles < 256 ? tiles : 256)), dim3(256), kPfLds,
-                               st, a);
+            if (gather) hipLaunchKernelGGL(gmsq_prefill_fixup_kernel<true>, fix_grid, dim3(256), kPfLds, st, a);
+            else hipLaunchKernelGGL(gmsq_prefill_fixup_kernel<false>, fix_grid, dim3(256), kPfLds, st, a);
             return check_launch();
         }
     }
