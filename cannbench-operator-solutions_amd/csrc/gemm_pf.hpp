@@ -1,0 +1,281 @@
+// gemm_pf.hpp - persistent int8 GEMM with the dequant epilogue (QuantMatmul, the grouped
+// down-projection GroupedMatmulQuant) on the GroupedMatmulSwigluQuant prefill core.
+//
+// Reference being replaced: the cube GEMM + vector dequant of quant_matmul (quant_matmul_plugin.cpp
+// launch path) and of the grouped int8 matmul; here the int32 product never leaves the registers.
+//
+// Core (gmsq_prefill.hpp): 256 x 256 tiles, four waves of 128 x 128 (v_mfma_i32_32x32x32_i8), K in
+// 64-deep stages through a 4-slot LDS ring fed by buffer_load ... lds, the DMAs of a stage spread
+// over the MFMAs of the previous one, and one continuous stage stream per workgroup: the last
+// iterations of a tile fetch the next tile's first 3.5 stages.  The column tile is folded into the
+// weight resource (its base is the tile's first column), so the per-lane chunk offsets are the
+// same for every tile of the launch.
+//
+// Epilogue, register direct (the ring already receives the next tile's stages): the dequant chain
+// of apply_deq per element (the common chain - per-channel scale, optional per-token scale, bf16
+// out - without the selects), a 4 x 4 transpose of 16-bit values across each lane quad so that a
+// lane holds 4 consecutive columns of one row, and 8-byte stores through a resource over the
+// tile's valid rows (columns past N go outside it).
+#pragma once
+
+#include "gmsq_prefill.hpp"
+
+namespace cb {
+
+constexpr int kGpfLds = kPfRing + 2 * kPfScSlot;  // the ring, then two scale slots
+
+// The tile's plan: rows [m0, m0 + vrows) of group g, column tile nt.
+struct GpfTile {
+    int g, m0, vrows, nt;
+};
+
+#ifndef CB_GPF_G
+#define CB_GPF_G 8
+#endif
+// Launch order.  Tiles k are numbered row-group major: groups of G consecutive row tiles, within a
+// group column tile by column tile, row tile fastest - G consecutive tiles share a weight slab.
+// Slot p (workgroup blockIdx.x walks p = blockIdx.x, + gridDim.x, ...; it runs on XCD p % 8 when
+// gridDim.x is a multiple of 8) takes tile k = G (8 (q / G) + p % 8) + q % G with q = p / 8: each
+// run of G tiles sharing a weight slab goes to one XCD, whose workgroups run it together, so the
+// slab crosses into one L2 once.  Slots past the padded count or with k >= T take no tile.
+constexpr int kGpfG = CB_GPF_G;
+
+__device__ __forceinline__ int gpf_k_of_slot(const int p)
+{
+    const int x = p & 7, q = p >> 3;
+    return kGpfG * (8 * (q / kGpfG) + x) + q % kGpfG;
+}
+
+__device__ __forceinline__ GpfTile gpf_tile(const GemmArgs& a, const int k)
+{
+    const int T_m = a.gt.total_mtiles, T_n = a.ntiles;
+    const int per_group = kGpfG * T_n;
+    const int first_m = (k / per_group) * kGpfG;
+    const int gsz = (T_m - first_m) < kGpfG ? (T_m - first_m) : kGpfG;
+    const int mt = first_m + (k % per_group) % gsz;
+    GpfTile t;
+    t.nt = (k % per_group) / gsz;
+    t.g = group_of_tile(a.gt, mt);
+    t.m0 = (t.g ? a.gt.row_end[t.g - 1] : 0) + (mt - a.gt.tile_start[t.g]) * 256;
+    t.vrows = a.gt.row_end[t.g] - t.m0;
+    return t;
+}
+
+// The first slot p' >= p (in steps of the grid) whose tile exists, or -1.
+__device__ __forceinline__ int gpf_next_slot(int p, const int step, const int slots, const int total)
+{
+    for (; p < slots; p += step)
+        if (gpf_k_of_slot(p) < total) return p;
+    return -1;
+}
+
+__device__ __forceinline__ PfSrc gpf_src(const GemmArgs& a, const GpfTile& t)
+{
+    PfSrc s;
+    const int64_t K = a.K, N = a.N;
+    const int64_t c0 = (int64_t)t.nt * 256;
+    s.ares = make_rsrc(a.x + (int64_t)t.m0 * K, (uint32_t)((int64_t)(t.vrows < 256 ? t.vrows : 256) * K));
+    s.bres = make_rsrc(a.w + (int64_t)t.g * a.w_gstride + c0, (uint32_t)(K * N - c0));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s.ga[i] = 0x80000000u;
+    return s;
+}
+
+// Row scale (the per-token scale, 1 without one) of tile row tid and column scale of tile column
+// tid, loaded into registers (every thread loads, absent operands through empty resources).
+__device__ __forceinline__ PfScales gpf_scales(const GemmArgs& a, const GpfTile& t)
+{
+    const EpiArgs& e = a.epi;
+    const int tid = opaque((int)threadIdx.x);
+    PfScales s;
+    const __amdgpu_buffer_rsrc_t pres =
+        e.has_pt ? make_rsrc(e.pertoken + t.m0, (uint32_t)((t.vrows < 256 ? t.vrows : 256) * 4)) : make_rsrc(a.x, 0u);
+    const float v = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(pres, (uint32_t)((tid < t.vrows ? tid : t.vrows - 1) * 4), 0, 0));
+    s.xs = e.has_pt ? v : 1.0f;
+    const int64_t cc = (int64_t)t.nt * 256 + tid;
+    const int64_t si = (int64_t)t.g * e.scale_gstride + (e.scale_perchan ? (cc < a.N ? cc : 0) : 0);
+    const __amdgpu_buffer_rsrc_t s32 = make_rsrc(e.scale, e.scale_bf16 ? 0u : 0x80000000u);
+    const __amdgpu_buffer_rsrc_t s16 = make_rsrc(e.scale, e.scale_bf16 ? 0x80000000u : 0u);
+    const float f32 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(s32, (uint32_t)(si * 4), 0, 0));
+    const uint16_t b16 = __builtin_amdgcn_raw_buffer_load_b16(s16, (uint32_t)(si * 2), 0, 0);
+    s.cs = e.scale_bf16 ? bf16_to_f32(b16) : f32;
+    return s;
+}
+
+// 16-bit 4 x 4 transpose across the lane quad (qi = lane % 4): on entry the lane holds rows
+// 0..3 of its column as p01 = rows 0, 1 and p23 = rows 2, 3; on exit d0, d1 hold row qi, columns
+// 0..3 of the quad.  Step 1 trades 2-row halves with lane qi ^ 2, step 2 single values with qi ^ 1;
+// the lane-dependent choices are selects and per-lane byte selectors of v_perm_b32 (sel_*), not
+// branches.
+struct Quad16Sel {
+    bool hi2;
+    u32 s_send, s_d0, s_d1;
+};
+
+__device__ __forceinline__ Quad16Sel quad16_sel(const int qi)
+{
+    const bool odd = qi & 1;
+    Quad16Sel q;
+    q.hi2 = qi & 2;
+    q.s_send = odd ? 0x05040100u : 0x07060302u;  // perm(second, first): lo / hi halves of both
+    q.s_d0 = odd ? 0x03020504u : 0x05040100u;    // perm(r2, first)
+    q.s_d1 = odd ? 0x03020706u : 0x07060100u;    // perm(r2, second)
+    return q;
+}
+
+__device__ __forceinline__ void quad_transpose16(const u32 p01, const u32 p23, const Quad16Sel& q, u32& d0, u32& d1)
+{
+    const u32 recv = (u32)__builtin_amdgcn_mov_dpp((int)(q.hi2 ? p01 : p23), 0x4E, 0xF, 0xF, false);
+    // first: column qi & 1, second: column (qi & 1) + 2, both for the lane pair's two rows
+    const u32 first = q.hi2 ? recv : p01, second = q.hi2 ? p23 : recv;
+    const u32 r2 = (u32)__builtin_amdgcn_mov_dpp((int)__builtin_amdgcn_perm(second, first, q.s_send), 0xB1, 0xF,
+                                                     0xF, false);
+    d0 = __builtin_amdgcn_perm(r2, first, q.s_d0);
+    d1 = __builtin_amdgcn_perm(r2, second, q.s_d1);
+}
+
+// Two values rounded to bf16 (round to nearest even) in one dword, the first in the low half.
+__device__ __forceinline__ u32 pack_bf16x2(const float a, const float b)
+{
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(u32, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+
+// The dequant epilogue of one tile from the accumulators.  Lane (h = lane / 32, c = lane % 32) of
+// fragment (fm, fn) holds rows (2 fm + wm) * 32 + 8 (r / 4) + 4 h + r % 4, column
+// tcol(fn) + c with tcol(fn) = 128 (fn / 2) + 64 wn + 32 (fn % 2).
+template <bool SIMPLE>
+__device__ __forceinline__ void gpf_epilogue(const GemmArgs& a, uint8_t* smem, v16i (&acc)[4][4], const GpfTile& t,
+                                             const int par)
+{
+    const int tid = opaque((int)threadIdx.x), lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const EpiArgs& e = a.epi;
+    const int64_t N = a.N;
+    const int h = lane >> 5, c = lane & 31, qi = c & 3;
+    const Quad16Sel qs = quad16_sel(qi);
+    const CB_LDS float* xs_l = (const CB_LDS float*)((CB_LDS uint8_t*)smem + kPfSc + par * kPfScSlot);
+    const CB_LDS float* cs_l = xs_l + 256;
+    const int vr = t.vrows < 256 ? t.vrows : 256;
+    const __amdgpu_buffer_rsrc_t ores = make_rsrc((uint16_t*)e.out + (int64_t)t.m0 * N, (uint32_t)((int64_t)vr * N * 2));
+    ColDeq cd[4];
+    uint32_t coff[4];
+#pragma unroll
+    for (int fn = 0; fn < 4; ++fn) {
+        const int tc = (fn >> 1) * 128 + wn * 64 + (fn & 1) * 32;
+        const int64_t cc = (int64_t)t.nt * 256 + tc + c;       // this lane's column (values)
+        const int64_t cq = (int64_t)t.nt * 256 + tc + (c & ~3);  // the quad's first column (stores)
+        if constexpr (SIMPLE) cd[fn] = ColDeq{cs_l[tc + c], 0.0f, 0.0f};
+        else cd[fn] = col_deq(e, t.g, 0, cc < N ? cc : 0);
+        coff[fn] = cq < N ? (uint32_t)cq * 2u : 0x80000000u;
+    }
+#pragma unroll
+    for (int fm = 0; fm < 4; ++fm) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int row = (2 * fm + wm) * 32 + 8 * q + 4 * h;  // rows row .. row + 3
+            const v4f xs4 = *(const CB_LDS v4f*)(xs_l + row);
+            const uint32_t roff = (uint32_t)(row + qi) * (uint32_t)N * 2u;
+#pragma unroll
+            for (int fn = 0; fn < 4; ++fn) {
+                float f[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int acc_v = acc_read(acc[fm][fn][4 * q + i]);
+                    if constexpr (SIMPLE) f[i] = ((float)acc_v * cd[fn].scale) * xs4[i];
+                    else f[i] = apply_deq(e, cd[fn], acc_v, xs4[i]);
+                }
+                u32 p01, p23;
+                if (SIMPLE || e.out_bf16) {
+                    p01 = pack_bf16x2(f[0], f[1]);
+                    p23 = pack_bf16x2(f[2], f[3]);
+                } else {
+                    p01 = (u32)f32_to_f16(f[0]) | ((u32)f32_to_f16(f[1]) << 16);
+                    p23 = (u32)f32_to_f16(f[2]) | ((u32)f32_to_f16(f[3]) << 16);
+                }
+                u32 d0, d1;
+                quad_transpose16(p01, p23, qs, d0, d1);
+                typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+                __builtin_amdgcn_raw_buffer_store_b64(v2u{d0, d1}, ores, roff + coff[fn], 0, 0);
+            }
+        }
+    }
+}
+
+// Persistent launch: gridDim.x workgroups (at most one per CU) walk the launch order's slots.
+// Batch 1, K of at least 4 stages, N a multiple of 4 (8-byte stores), bf16 / fp16 out.
+template <bool SIMPLE>
+__global__ __launch_bounds__(256, 1) void gpf_dequant_kernel(const GemmArgs a)
+{
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    const int total = a.gt.total_mtiles * a.ntiles;
+    const int slots = (total + 8 * kGpfG - 1) / (8 * kGpfG) * (8 * kGpfG);
+    const int step = (int)gridDim.x;
+    int pid = gpf_next_slot((int)blockIdx.x, step, slots, total);
+    if (pid < 0) return;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    uint32_t a_rd[4][2], b_rd[4];
+    pf_read_offsets(wm, wn, lane, a_rd, b_rd);
+    const int nk = __builtin_amdgcn_readfirstlane((int)((a.K + PfCfg::BK - 1) / PfCfg::BK));
+    const PfOffs offs = pf_offsets<false, false>(a, 0, wave, lane);
+    auto put_scales = [&](const PfScales& v, int par) {
+        CB_LDS float* sl = (CB_LDS float*)((CB_LDS uint8_t*)smem + kPfSc + par * kPfScSlot);
+        sl[tid] = v.xs;
+        sl[256 + tid] = v.cs;
+    };
+    GpfTile cur_t = gpf_tile(a, gpf_k_of_slot(pid));
+    PfSrc cur = gpf_src(a, cur_t);
+    pf_prologue<false>(cur, offs, nk, smem, wave);
+    put_scales(gpf_scales(a, cur_t), 0);
+    int par = 0, rb = 0;
+    bool first = true;
+    for (;;) {
+        const int pn = gpf_next_slot(pid + step, step, slots, total);
+        const bool has_nxt = pn >= 0;
+        GpfTile nxt_t;
+        PfSrc nxt;
+        PfScales nsc;
+        if (has_nxt) {
+            nxt_t = gpf_tile(a, gpf_k_of_slot(pn));
+            nxt = gpf_src(a, nxt_t);
+            nsc = gpf_scales(a, nxt_t);
+        } else {
+            nxt = pf_dead(a);
+        }
+        v16i acc[4][4];
+#pragma unroll
+        for (int fm = 0; fm < 4; ++fm)
+#pragma unroll
+            for (int fn = 0; fn < 4; ++fn)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0;
+        const int nblk = (cur_t.vrows + 31) / 32;
+        const int nv = __builtin_amdgcn_readfirstlane(nblk > wm ? min((nblk - wm + 1) / 2, 4) : 0);
+        // A later tile's loop starts with wait vmcnt(63): its first 28 DMAs were issued before the
+        // previous epilogue's 64 stores, so at most 63 outstanding operations means they landed.
+        if (nv >= 4) pf_kloop<4, true, false>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+        else if (nv == 3) pf_kloop<3, true, false>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+        else if (nv == 2) pf_kloop<2, true, false>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+        else if (nv == 1) pf_kloop<1, true, false>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+        else pf_kloop<0, true, false>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+        gpf_epilogue<SIMPLE>(a, smem, acc, cur_t, par);
+        if (has_nxt) put_scales(nsc, par ^ 1);
+        // every wave is past this epilogue's scale reads (and the next scales are written) before
+        // the next tile's epilogue; no global load in between, so no wait on the stores
+        __syncthreads();
+        if (!has_nxt) break;
+        rb = (rb + nk) & 3;
+        par ^= 1;
+        cur = nxt;
+        cur_t = nxt_t;
+        pid = pn;
+        first = false;
+    }
+}
+
+}  // namespace cb

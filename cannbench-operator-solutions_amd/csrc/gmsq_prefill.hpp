@@ -57,7 +57,10 @@ struct PfSrc {
     uint32_t ga[4];  // GATHER: source row * K of each A chunk (0x80000000: no row)
 };
 
-template <bool GATHER>
+// SW (GroupedMatmulSwigluQuant): the stage's 256 columns are the column tile nt's 128 gate columns
+// then the matching 128 up columns.  Otherwise 256 consecutive columns from the start of the
+// weight resource, which the caller places at the tile's first column.
+template <bool GATHER, bool SW = true>
 __device__ __forceinline__ PfOffs pf_offsets(const GemmArgs& a, const int nt, const int wave, const int lane)
 {
     PfOffs o;
@@ -74,10 +77,14 @@ __device__ __forceinline__ PfOffs pf_offsets(const GemmArgs& a, const int nt, co
     for (int i = 0; i < 4; ++i) {
         const int cid = (i * 4 + wave) * 64 + lane;
         const int row = cid >> 4, pos = cid & 15;
-        const int c = pos ^ ((row & 7) << 1);  // logical 16-column chunk: gate (c < 8) or up
-        const int64_t j = (int64_t)nt * 128 + 16 * (c & 7);
-        const int64_t col = c < 8 ? j : a.epi.H + j;
-        o.b[i] = (uint32_t)row * o.n + (uint32_t)(j < a.epi.H ? col : 0);
+        const int c = pos ^ ((row & 7) << 1);  // logical 16-column chunk (SW: gate c < 8, else up)
+        if constexpr (SW) {
+            const int64_t j = (int64_t)nt * 128 + 16 * (c & 7);
+            const int64_t col = c < 8 ? j : a.epi.H + j;
+            o.b[i] = (uint32_t)row * o.n + (uint32_t)(j < a.epi.H ? col : 0);
+        } else {
+            o.b[i] = (uint32_t)row * o.n + (uint32_t)(16 * c);
+        }
     }
     return o;
 }

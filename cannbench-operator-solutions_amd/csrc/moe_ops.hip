@@ -12,6 +12,7 @@
 
 #include "gmsq_decode.hpp"
 #include "gmsq_prefill.hpp"
+#include "gemm_pf.hpp"
 
 namespace cb {
 
@@ -150,6 +151,20 @@ static void launch_gemm(GemmArgs& a, const int64_t* gl, int64_t E, int64_t batch
     a.ntiles = (int)((Ncols + 255) / 256);
     const int64_t blocks = (int64_t)a.gt.total_mtiles * a.ntiles;
     const int pg = persistent_grid();
+    if constexpr (EPI == EPI_DEQUANT) {
+        // the four-wave ring core with a continuous stage stream (K of at least 4 stages) and
+        // 8-byte stores of 4 columns (N a multiple of 4)
+        if (batch == 1 && pg > 0 && a.K >= 4 * PfCfg::BK && Ncols % 4 == 0 && 256 * Ncols * 2 < 0x7fffffffLL) {
+            const EpiArgs& e = a.epi;
+            const bool simple = !e.has_offset && e.bias_kind == BIAS_NONE && e.out_bf16;
+            const void* kern = simple ? (const void*)gpf_dequant_kernel<true> : (const void*)gpf_dequant_kernel<false>;
+            allow_dynamic_lds(kern, kGpfLds);
+            const dim3 grid((unsigned)(blocks < pg ? blocks : pg));
+            if (simple) hipLaunchKernelGGL(gpf_dequant_kernel<true>, grid, dim3(256), kGpfLds, st, a);
+            else hipLaunchKernelGGL(gpf_dequant_kernel<false>, grid, dim3(256), kGpfLds, st, a);
+            return;
+        }
+    }
     // persistent launch once there are more tiles than workgroups (one continuous DMA stream per
     // workgroup: a tile's last STAGES iterations issue the next tile's first STAGES stages, so K
     // must span at least STAGES stages); its register-direct epilogue addresses a tile's rows with
