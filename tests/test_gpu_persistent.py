@@ -1,8 +1,7 @@
 """GPU parity of the persistent dequant / int32 GEMM (one continuous DMA stage stream per workgroup).
 
-The default launch goes persistent only when a problem has more tiles than the device has CUs, so
-these tests force a small grid with the library's test override: every workgroup then walks many
-tiles.  Together the cases cover an odd number of K stages (the ring rotates between tiles), K of
+These tests force a small grid with the library's test override, so every workgroup walks many
+tiles (the dequant GEMM on the ring core and the 8-wave int32 GEMM).  Together the cases cover an odd number of K stages (the ring rotates between tiles), K of
 exactly the ring's depth, K shorter than the ring (launched one tile per workgroup instead), ragged
 and empty groups, partial row and column tiles, every dequant flag, and the last tile's stages that
 fetch nothing.  The bar is the same as the non-persistent path: bit-exact against the oracle.
@@ -37,7 +36,8 @@ def small_grid(request, overrides):
 
 
 GMQ_CASES = [
-    # (counts, K, N): K stages of 128 -> 3 (odd), 4, 2 (the ring's depth), 1 (not persistent)
+    # (counts, K, N): 64-deep stages of the ring-core dequant kernel -> 6, 7 (odd: the ring slot
+    # rotates by 3 per tile), 4 (exactly its prologue depth), 2 (below it: the 8-wave kernel)
     ([300, 0, 45, 600, 1, 0, 33], 384, 784),
     ([270, 40], 400, 784),
     ([520, 17, 0], 256, 512),
