@@ -515,26 +515,27 @@ __device__ __forceinline__ float from_agpr(float v)
 }
 
 // One step of a half-wave max over non-negative float bit patterns held as u32 (integer max needs
-// no NaN canonicalisation, so each step is one v_max_u32 with a DPP source).  mov_dpp leaves the
-// lanes it does not write undefined.
+// no NaN canonicalisation).  The DPP move with a zero old value and bound_ctrl folds into the max:
+// one v_max_u32_dpp per step.  Lanes outside ROWS see 0 and keep their own value.
 template <int CTRL, int ROWS>
 __device__ __forceinline__ u32 umax_dpp(u32 v)
 {
-    const u32 o = (u32)__builtin_amdgcn_mov_dpp((int)v, CTRL, ROWS, 0xF, false);
+    const u32 o = (u32)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xF, true);
     return v > o ? v : o;
 }
 
-// rint16 of four values packed into the four bytes of a dword: fp16 rounding (v_cvt_f16_f32),
-// fp16 round-half-even, fp16 -> int16 (NaN -> 0, +-inf saturate), then a clamp to [-128, 127]:
-// the same steps as rint16 in one fewer pass through fp32.
+// rint16 for the requant's products v = act * (127 / amax) of one row: fp16 rounding
+// (v_cvt_f16_f32), fp16 round-half-even, fp16 -> int16 (NaN -> 0).  |act| <= amax for every act of
+// the row (amax is their maximum, NaN ignored), so |v| <= 127 (1 + 2^-23) and the fp16 value lies
+// in [-127, 127]: rint16's clamp to [-128, 127] never acts and is left out.  Only the low byte of
+// the result is used.
 __device__ __forceinline__ int rint16_h(float v)
 {
     // opaque: v is the rounded fp32 product, not folded into a mixed-precision fma with one rounding
     const _Float16 r = __builtin_elementwise_roundeven((_Float16)opaque(v));
     int i;
     asm("v_cvt_i16_f16 %0, %1" : "=v"(i) : "v"(r));
-    const short s = (short)i;
-    return s < -128 ? -128 : (s > 127 ? 127 : s);
+    return i;
 }
 
 // One persistent GMSQ tile after its K loop: everything from the SwiGLU to the int8 stores.
