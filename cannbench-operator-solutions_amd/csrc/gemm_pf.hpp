@@ -247,13 +247,7 @@ __global__ __launch_bounds__(256, 1) void gpf_dequant_kernel(const GemmArgs a)
         } else {
             nxt = pf_dead(a);
         }
-        v16i acc[4][4];
-#pragma unroll
-        for (int fm = 0; fm < 4; ++fm)
-#pragma unroll
-            for (int fn = 0; fn < 4; ++fn)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0;
+        v16i acc[4][4];  // defined by the K loop (its first MFMAs start from zero)
         const int nblk = (cur_t.vrows + 31) / 32;
         const int nv = __builtin_amdgcn_readfirstlane(nblk > wm ? min((nblk - wm + 1) / 2, 4) : 0);
         // A later tile's loop starts with wait vmcnt(63): its first 28 DMAs were issued before the

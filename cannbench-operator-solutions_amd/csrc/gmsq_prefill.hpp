@@ -337,11 +337,15 @@ __device__ __forceinline__ void pf_kloop(const PfSrc& dma, const PfSrc& nxt, con
     auto rda = [&](int kt, int ks, int fm, v4i (&af)[NVA]) {
         if (fm < NV) af[fm < NVA ? fm : 0] = *(const CB_LDS v4i*)(sm + ((rb + kt) & 3) * C::STAGE + a_rd[fm][ks]);
     };
-    auto mrow = [&](int fm, const v4i (&af)[NVA], const v4i (&bf)[4]) {
+    // ZERO: the tile's first MFMAs, which start from a zero accumulator (no separate clearing of
+    // the 256 accumulator registers)
+    auto mrow = [&](int fm, const v4i (&af)[NVA], const v4i (&bf)[4], auto zero_t) {
+        constexpr bool ZERO = decltype(zero_t)::value;
         if (fm < NV) {
 #pragma unroll
             for (int fn = 0; fn < 4; ++fn)
-                acc[fm][fn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[fm < NVA ? fm : 0], bf[fn], acc[fm][fn], 0, 0, 0);
+                acc[fm][fn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[fm < NVA ? fm : 0], bf[fn],
+                                                                    ZERO ? v16i{} : acc[fm][fn], 0, 0, 0);
         }
     };
     // one chunk: a DMA, then its fragment reads interleaved one for one with 4 MFMAs; chunks are
@@ -368,55 +372,73 @@ __device__ __forceinline__ void pf_kloop(const PfSrc& dma, const PfSrc& nxt, con
 #pragma unroll
         for (int c = 0; c < 4; ++c) rda(0, 0, c, a0);
     }
-#pragma nounroll
-    for (int kt = 0; kt < nk; ++kt) {
-        int sb, sa;
+    using F = std::integral_constant<bool, false>;
+    using T = std::integral_constant<bool, true>;
+    // half 1 of iteration kt: MFMAs of step 0 (a0/b0), reads of step 1, the B chunks of stage kt + 3
+    auto half1 = [&](const int kt, auto zero_t) {
+        int sb;
         const PfSrc db = pf_stream<PF>(dma, nxt, kt + 3, nk, sb);
-        const PfSrc da = pf_stream<PF>(dma, nxt, kt + 4, nk, sa);
-        // half 1: MFMAs of step 0 (a0/b0), reads of step 1, the B chunks of stage kt + 3
         const int s3 = (rb + kt + 3) & 3;
         pf_dma<4, GATHER, !PF>(db, offs, sb, nk, s3, lds_base, wave);
         if constexpr (NV > 0) { rdb(kt, 1, 0, b1); rdb(kt, 1, 1, b1); }
-        mrow(0, a0, b0);
+        mrow(0, a0, b0, zero_t);
         fence();
         pf_dma<5, GATHER, !PF>(db, offs, sb, nk, s3, lds_base, wave);
         if constexpr (NV > 0) { rdb(kt, 1, 2, b1); rdb(kt, 1, 3, b1); }
-        mrow(1, a0, b0);
+        mrow(1, a0, b0, zero_t);
         fence();
         pf_dma<6, GATHER, !PF>(db, offs, sb, nk, s3, lds_base, wave);
         rda(kt, 1, 0, a1);
         rda(kt, 1, 1, a1);
-        mrow(2, a0, b0);
+        mrow(2, a0, b0, zero_t);
         fence();
         pf_dma<7, GATHER, !PF>(db, offs, sb, nk, s3, lds_base, wave);
         rda(kt, 1, 2, a1);
         rda(kt, 1, 3, a1);
-        mrow(3, a0, b0);
+        mrow(3, a0, b0, zero_t);
         fence();
-        // stage kt + 1 landed (outstanding: stage kt + 2 and kt + 3), stage kt fully read
+    };
+    // half 2 of iteration kt: stage kt + 1 landed (outstanding: stage kt + 2 and kt + 3) and stage
+    // kt fully read; MFMAs of step 1 (a1/b1), reads of stage kt + 1 step 0, the A chunks of stage
+    // kt + 4 into the slot stage kt just left
+    auto half2 = [&](const int kt) {
         wait_vmcnt_barrier<2 * C::ISSUE>();
-        // half 2: MFMAs of step 1 (a1/b1), reads of stage kt + 1 step 0, the A chunks of stage
-        // kt + 4 into the slot stage kt just left
+        int sa;
+        const PfSrc da = pf_stream<PF>(dma, nxt, kt + 4, nk, sa);
         const int s4 = (rb + kt) & 3;
         pf_dma<0, GATHER, !PF>(da, offs, sa, nk, s4, lds_base, wave);
         if constexpr (NV > 0) { rdb(kt + 1, 0, 0, b0); rdb(kt + 1, 0, 1, b0); }
-        mrow(0, a1, b1);
+        mrow(0, a1, b1, F());
         fence();
         pf_dma<1, GATHER, !PF>(da, offs, sa, nk, s4, lds_base, wave);
         if constexpr (NV > 0) { rdb(kt + 1, 0, 2, b0); rdb(kt + 1, 0, 3, b0); }
-        mrow(1, a1, b1);
+        mrow(1, a1, b1, F());
         fence();
         pf_dma<2, GATHER, !PF>(da, offs, sa, nk, s4, lds_base, wave);
         rda(kt + 1, 0, 0, a0);
         rda(kt + 1, 0, 1, a0);
-        mrow(2, a1, b1);
+        mrow(2, a1, b1, F());
         fence();
         pf_dma<3, GATHER, !PF>(da, offs, sa, nk, s4, lds_base, wave);
         rda(kt + 1, 0, 2, a0);
         rda(kt + 1, 0, 3, a0);
-        mrow(3, a1, b1);
+        mrow(3, a1, b1, F());
         fence();
+    };
+    // fragments without valid rows get no MFMAs: their accumulators are plain zeros
+#pragma unroll
+    for (int fm = NV; fm < 4; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < 4; ++fn) acc[fm][fn] = v16i{};
+    // the loop rotated by half an iteration, so that the tile's first half-step (the MFMAs from a
+    // zero accumulator) stands outside it
+    half1(0, T());
+#pragma nounroll
+    for (int kt = 0; kt < nk - 1; ++kt) {
+        half2(kt);
+        half1(kt + 1, F());
     }
+    half2(nk - 1);
 }
 
 // Prologue of a tile: stages 0-2 and the A chunks of stage 3 (the loop issues the rest).
@@ -778,13 +800,7 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_kernel(const GemmArgs a)
         } else {
             nxt = pf_dead(a);
         }
-        v16i acc[4][4];
-#pragma unroll
-        for (int fm = 0; fm < 4; ++fm)
-#pragma unroll
-            for (int fn = 0; fn < 4; ++fn)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0;
+        v16i acc[4][4];  // defined by the K loop (its first MFMAs start from zero)
         // 32-row blocks with valid rows: wave row wm multiplies fragments fm with 2 fm + wm < nblk
         const int nblk = (cur_t.vrows + 31) / 32;
         const int nv = __builtin_amdgcn_readfirstlane(nblk > wm ? min((nblk - wm + 1) / 2, 4) : 0);
@@ -852,13 +868,7 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_fixup_kernel(const GemmAr
             sl[tid] = sc.xs;
             sl[256 + tid] = sc.cs;
         }
-        v16i acc[4][4];
-#pragma unroll
-        for (int fm = 0; fm < 4; ++fm)
-#pragma unroll
-            for (int fn = 0; fn < 4; ++fn)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[fm][fn][r] = 0;
+        v16i acc[4][4];  // defined by the K loop (its first MFMAs start from zero)
         pf_kloop<4, false, GATHER>(cur, cur, offs, nk, 0, smem, a_rd, b_rd, acc, wave, true);
         pf_epilogue<true>(a, smem, acc, tl, nt, 0, 0, 0, t);
         __syncthreads();
