@@ -489,7 +489,8 @@ __device__ __forceinline__ PfScales pf_scales(const GemmArgs& a, const PfTile& t
 }
 
 // Per-lane LDS read offsets of the fragments (stage-relative).  A: fragment fm of wave row wm
-// covers tile rows (2 fm + wm) * 32 + lane % 32, k chunk 2 ks + lane / 32.  B: see TileDma.
+// covers tile rows (2 fm + wm) * 32 + lane % 32, k chunk 2 ks + lane / 32.  B: the transposing
+// read of gemm_lds.hpp (one base offset per fragment, the rest are instruction immediates).
 __device__ __forceinline__ void pf_read_offsets(int wm, int wn, int lane, uint32_t (&a_rd)[4][2], uint32_t (&b_rd)[4])
 {
     using C = PfCfg;
