@@ -92,6 +92,31 @@ def test_exchange_timeout_fixup(cb, orc, overrides, counts, K, N):
     assert gave_up in (0, 1)
 
 
+@pytest.mark.parametrize("counts,K,N,T", [
+    ([300, 0, 700, 45, 1000], 512, 4096, 900),   # prefill kernel with gathered rows
+    ([5, 0, 17, 32, 1, 9] * 8, 448, 4096, 200),  # decode kernel with gathered rows
+])
+def test_gather_exchange_timeout_fixup(cb, overrides, counts, K, N, T):
+    """The gathered variants under a one-poll exchange limit: the fix-up launches recompute the
+    tiles that gave up through the same row index, so the outputs equal the normal run's."""
+    g = cpu_gen(T + K)
+    E, M = len(counts), sum(counts)
+    x = rand_i8((T, K), g)
+    w = rand_i8((E, K, N), g)
+    ws = (torch.rand(E, N, generator=g) * 0.009 + 0.001).to(DEV)
+    xs = (torch.rand(T, generator=g) * 0.015 + 0.005).to(DEV)
+    idx = torch.randint(0, T, (M,), generator=g, dtype=torch.int32).to(DEV)
+    gl = np.cumsum(counts).tolist()
+    y0, ys0 = cb.grouped_matmul_swiglu_quant_gather(x, idx, w, ws, xs, gl)
+    torch.cuda.synchronize()
+    overrides(exchange_spin_limit=1)
+    y1, ys1 = cb.grouped_matmul_swiglu_quant_gather(x, idx, w, ws, xs, gl)
+    torch.cuda.synchronize()
+    overrides()
+    assert torch.equal(y0, y1)
+    assert torch.equal(ys0, ys1)
+
+
 def test_decode_exchange_waits_for_every_lane(cb, orc):
     """Every row of a 16-row block must wait for all of its column tiles' maxima, the rows held by
     lanes 32-63 of a wave (block positions 8-15) included: a wait that decided on the lower 32
