@@ -735,8 +735,8 @@ __device__ __forceinline__ void pf_epilogue(const GemmArgs& a, uint8_t* smem, v1
 }
 
 // Persistent GroupedMatmulSwigluQuant prefill kernel.  gridDim.x workgroups, at most one per CU,
-// all resident together (the host checks the occupancy).  Exchange group q = round q of slot s:
-// its RT row tiles x ntl column tiles meet at arrive[q] once per round.  GATHER: activation rows
+// all resident together (the host checks the occupancy).  Exchange group: the row maxima of
+// row tile mt are final once its ntl column tiles have counted at arrive[mt].  GATHER: activation rows
 // through the row index.
 template <bool GATHER>
 __global__ __launch_bounds__(256, 1) void gmsq_prefill_kernel(const GemmArgs a)
@@ -750,7 +750,7 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_kernel(const GemmArgs a)
     CB_LDS int* tab = (CB_LDS int*)((CB_LDS uint8_t*)smem + kPfOrd);
     const PfOrder ord = pf_build_order(a.gt, pl.RT, tab);
     const int rounds = pf_total_rounds(ord);
-    const u32 target = (u32)(pl.RT * ntl);
+    const u32 target = (u32)ntl;  // a row tile's column tiles meet at arrive[mt]
     uint32_t a_rd[4][2], b_rd[4];
     pf_read_offsets(wm, wn, lane, a_rd, b_rd);
     const int nk = __builtin_amdgcn_readfirstlane((int)((a.K + PfCfg::BK - 1) / PfCfg::BK));
@@ -782,8 +782,7 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_kernel(const GemmArgs a)
         const int qn = q + pl.slots;
         const PfTile nxt_t = pf_round_tile(a.gt, tab, ord, pl.RT, qn, pl.rt);
         if (cur_t.mt < 0) {
-            // past the last row tile of its kind: still take part in the round's exchange
-            if (tid == 0) __hip_atomic_fetch_add(a.epi.arrive + q, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // past the last row tile of its kind (no exchange: the counters are per row tile)
             if (nxt_t.mt >= 0) {
                 __syncthreads();
                 cur = pf_src<GATHER>(a, nxt_t.g, nxt_t.m0, nxt_t.vrows, wave, opaque(lane));
@@ -826,7 +825,7 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_kernel(const GemmArgs a)
             else if (nv == 1) pf_kloop<1, false, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
             else pf_kloop<0, false, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
         }
-        pf_epilogue<false>(a, smem, acc, cur_t, pl.nt, par, q, target, cur_t.mt * ntl + pl.nt);
+        pf_epilogue<false>(a, smem, acc, cur_t, pl.nt, par, cur_t.mt, target, cur_t.mt * ntl + pl.nt);
         if (nxt_t.mt >= 0) put_scales(nsc, par ^ 1);
         // every wave is past its LDS reads of this epilogue (and the next scales are written)
         // before the next tile's epilogue
