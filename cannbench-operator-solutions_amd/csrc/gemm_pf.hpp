@@ -222,7 +222,7 @@ __global__ __launch_bounds__(256, 1) void gpf_dequant_kernel(const GemmArgs a)
     uint32_t a_rd[4][2], b_rd[4];
     pf_read_offsets(wm, wn, lane, a_rd, b_rd);
     const int nk = __builtin_amdgcn_readfirstlane((int)((a.K + PfCfg::BK - 1) / PfCfg::BK));
-    const PfOffs offs = pf_offsets<false, false>(a, 0, wave, lane);
+    const PfOffs offs = pf_offsets<false, false>(a, wave, lane);
     auto put_scales = [&](const PfScales& v, int par) {
         CB_LDS float* sl = (CB_LDS float*)((CB_LDS uint8_t*)smem + kPfSc + par * kPfScSlot);
         sl[tid] = v.xs;

@@ -26,14 +26,18 @@
 // written during the previous tile's epilogue):
 //   1. SwiGLU from the accumulators (the reference's operation order), |act| row maxima reduced
 //      across lanes (DPP) and across the two waves sharing rows (LDS), one device-scope atomicMax
-//      per (row, tile);
-//   2. arrival count for the round's exchange group, then a bounded wait until every column tile
-//      of the group's row tiles has published;
-//   3. per-row 127 / amax through LDS, rint16 in registers, a 4 x 4 byte transpose across each
-//      lane quad, and dword stores of int8 y (four consecutive columns per lane).
-// A column tile whose wait times out marks itself in the workspace and stores nothing; the fix-up
-// launch that always follows recomputes exactly those tiles with the final row maxima, so the
-// output is right whatever the residency of the grid (it exits at once when nothing is marked).
+//      per (row, tile), one arrival on the row tile's counter;
+//   2. the activations stay in VGPRs through the workgroup's next K loop; after it, the row tile's
+//      counter is checked (its other 15 column tiles have normally arrived long before), and the
+//      tile is requantised: per-row 127 / amax through LDS, rint16 in registers, a 4 x 4 byte
+//      transpose across each lane quad, dword stores of int8 y (four consecutive columns per lane).
+// The column tile of a workgroup rotates by one per round, so the two column tiles whose weight
+// lines read slowly fall to a different workgroup every round.  A column tile whose wait times out
+// marks itself in the workspace and stores nothing; the fix-up launch that always follows
+// recomputes exactly those tiles with the final row maxima, so the output is right whatever the
+// residency of the grid (it exits at once when nothing is marked).  K below 4 stages (no stage
+// stream across tiles) uses the lock-step form: each tile waits for its row tile's exchange and
+// requantises at once.
 #pragma once
 
 #include "gemm_lds.hpp"
@@ -48,56 +52,70 @@ using PfCfg = LdsCfg<2, 2, 4, 64>;
 // once per workgroup, and a tile contributes only its two buffer resources (PfSrc; rows past the
 // tile's valid rows lie outside the activation resource and read zeros).  Gathered rows (GATHER)
 // add per-tile source-row offsets.
+// Chunk i of a wave's 4 A (B) chunks lies i * ka (16 weight rows) bytes past chunk 0, so a lane keeps
+// one offset per operand and the rest is a scalar.
 struct PfOffs {
-    uint32_t a[4], b[4];
-    uint32_t n;  // weight row length
+    uint32_t a0, b0;
+    uint32_t ka;  // 64 activation rows (0 with GATHER: the row offsets are per chunk)
+    uint32_t n;   // weight row length
 };
 struct PfSrc {
     __amdgpu_buffer_rsrc_t ares, bres;
     uint32_t ga[4];  // GATHER: source row * K of each A chunk (0x80000000: no row)
 };
 
-// SW (GroupedMatmulSwigluQuant): the stage's 256 columns are the column tile nt's 128 gate columns
-// then the matching 128 up columns.  Otherwise 256 consecutive columns from the start of the
-// weight resource, which the caller places at the tile's first column.
+// SW (GroupedMatmulSwigluQuant): the stage's 256 columns are a column tile's 128 gate columns then
+// the matching 128 up columns, counted from the weight resource's base, which pf_src places at
+// the tile's first gate column (so these offsets are the same for every column tile).  Otherwise
+// 256 consecutive columns from the start of the weight resource, which the caller places at the
+// tile's first column.
 template <bool GATHER, bool SW = true>
-__device__ __forceinline__ PfOffs pf_offsets(const GemmArgs& a, const int nt, const int wave, const int lane)
+__device__ __forceinline__ PfOffs pf_offsets(const GemmArgs& a, const int wave, const int lane)
 {
     PfOffs o;
     const uint32_t K = (uint32_t)a.K;
     o.n = (uint32_t)a.N;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int cid = (i * 4 + wave) * 64 + lane;  // 16-byte chunk id in the A tile
+    o.ka = GATHER ? 0u : 64u * K;
+    {
+        // chunk 0: A tile row wave * 16 + lane / 4; the swizzle depends on lane / 16 only, so
+        // chunk i (row + 64 i) has the same 16-byte position
+        const int cid = wave * 64 + lane;  // 16-byte chunk id in the A tile
         const int row = cid >> 2, pos = cid & 3;
         const uint32_t q16 = (uint32_t)((pos ^ a_swizzle<4>(row)) * 16);
-        o.a[i] = GATHER ? q16 : (uint32_t)row * K + q16;
+        o.a0 = GATHER ? q16 : (uint32_t)row * K + q16;
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int cid = (i * 4 + wave) * 64 + lane;
+    {
+        // chunk 0: stage row wave * 4 + lane / 16; the swizzle key row & 7 is the same for
+        // chunk i (row + 16 i)
+        const int cid = wave * 64 + lane;
         const int row = cid >> 4, pos = cid & 15;
         const int c = pos ^ ((row & 7) << 1);  // logical 16-column chunk (SW: gate c < 8, else up)
         if constexpr (SW) {
-            const int64_t j = (int64_t)nt * 128 + 16 * (c & 7);
-            const int64_t col = c < 8 ? j : a.epi.H + j;
-            o.b[i] = (uint32_t)row * o.n + (uint32_t)(j < a.epi.H ? col : 0);
+            // past H (the last column tile when H % 128 != 0) these read other columns; their
+            // weight scales are 0, so those activations are 0 and never stored
+            const uint32_t j = 16 * (c & 7);
+            o.b0 = (uint32_t)row * o.n + (c < 8 ? j : (uint32_t)a.epi.H + j);
         } else {
-            o.b[i] = (uint32_t)row * o.n + (uint32_t)(16 * c);
+            o.b0 = (uint32_t)row * o.n + (uint32_t)(16 * c);
         }
     }
     return o;
 }
 
+// The plan of row tile (g, m0, vrows) x column tile nt.  The weight resource starts at the tile's
+// first gate column: a weight row k >= K then lies past its end (the resource is nt * 128 bytes
+// shorter), and so does no valid column of row K - 1 (nt * 128 + 128 <= H, or the columns are
+// past H).
 template <bool GATHER>
-__device__ __forceinline__ PfSrc pf_src(const GemmArgs& a, const int g, const int m0, const int vrows, const int wave,
-                                        const int lane)
+__device__ __forceinline__ PfSrc pf_src(const GemmArgs& a, const int g, const int m0, const int vrows, const int nt,
+                                        const int wave, const int lane)
 {
     PfSrc s;
     const int64_t K = a.K;
     s.ares = GATHER ? make_rsrc(a.x, (uint32_t)(a.x_rows * K))
                     : make_rsrc(a.x + (int64_t)m0 * K, (uint32_t)((int64_t)(vrows < 256 ? vrows : 256) * K));
-    s.bres = make_rsrc(a.w + (int64_t)g * a.w_gstride, (uint32_t)(K * a.N));
+    const int64_t c0 = (int64_t)nt * 128;
+    s.bres = make_rsrc(a.w + (int64_t)g * a.w_gstride + c0, (uint32_t)(K * a.N - c0));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         s.ga[i] = 0x80000000u;
@@ -131,11 +149,11 @@ __device__ __forceinline__ void pf_dma(const PfSrc& s, const PfOffs& o, const in
     using C = PfCfg;
     const uint32_t sa = lds_base + (uint32_t)(slot * C::STAGE);
     if constexpr (I < 4) {
-        uint32_t off = (GATHER ? s.ga[I] + o.a[I] : o.a[I]) + (uint32_t)(kt * C::BK);
+        uint32_t off = (GATHER ? s.ga[I] + o.a0 : o.a0) + ((uint32_t)I * o.ka + (uint32_t)(kt * C::BK));
         if (CHECK && kt >= nk) off = 0x80000000u;
         dma16(s.ares, off, __builtin_amdgcn_readfirstlane(sa + (uint32_t)((I * 4 + wave) * 1024)));
     } else {
-        dma16(s.bres, o.b[I - 4] + (uint32_t)(kt * C::BK) * o.n,
+        dma16(s.bres, o.b0 + (uint32_t)((I - 4) * 16 + kt * C::BK) * o.n,
               __builtin_amdgcn_readfirstlane(sa + C::A_BYTES + (uint32_t)(((I - 4) * 4 + wave) * 1024)));
     }
 }
@@ -146,7 +164,8 @@ __device__ __forceinline__ void pf_dma(const PfSrc& s, const PfOffs& o, const in
 constexpr int kPfRing = PfCfg::STAGES_ * PfCfg::STAGE;
 constexpr int kPfSc = kPfRing, kPfScSlot = 2048, kPfRm = kPfSc + 2 * kPfScSlot, kPfInv = kPfRm + 2048;
 constexpr int kPfOrd = kPfInv + 1024;
-constexpr int kPfLds = kPfOrd + 3 * 4 * (CB_MAX_EXPERTS + 1);
+constexpr int kPfFlag = kPfOrd + 3 * 4 * (CB_MAX_EXPERTS + 1);  // the deferred requant's exchange outcome
+constexpr int kPfLds = kPfFlag + 16;
 static_assert(PfCfg::A_ISSUE == 4 && PfCfg::B_ISSUE == 4 && PfCfg::NW == 4 && PfCfg::FM == 4 && PfCfg::FN == 4,
               "the stage schedule below is written for this configuration");
 
@@ -337,13 +356,17 @@ __device__ __forceinline__ void pf_kloop(const PfSrc& dma, const PfSrc& nxt, con
         bf[fn] = v4i{lo[0], lo[1], hi[0], hi[1]};
     };
     auto rda = [&](int kt, int ks, int fm, v4i (&af)[NVA]) {
-        if (fm < NV) af[fm < NVA ? fm : 0] = *(const CB_LDS v4i*)(sm + ((rb + kt) & 3) * C::STAGE + a_rd[fm][ks]);
+        // a_rd[fm][ks] = a_rd[0][ks] + fm * 64 rows (the swizzle depends on the row within its
+        // 32-row block only): an instruction immediate
+        if (fm < NV)
+            af[fm < NVA ? fm : 0] = *(const CB_LDS v4i*)(sm + ((rb + kt) & 3) * C::STAGE + a_rd[0][ks] + fm * 64 * C::BK);
     };
     // ZERO: the tile's first MFMAs, which start from a zero accumulator (no separate clearing of
     // the 256 accumulator registers)
-    auto mrow = [&](int fm, const v4i (&af)[NVA], const v4i (&bf)[4], auto zero_t) {
+    auto mrow = [&](auto fm_t, const v4i (&af)[NVA], const v4i (&bf)[4], auto zero_t) {
+        constexpr int fm = decltype(fm_t)::value;
         constexpr bool ZERO = decltype(zero_t)::value;
-        if (fm < NV) {
+        if constexpr (fm < NV) {
 #pragma unroll
             for (int fn = 0; fn < 4; ++fn)
                 acc[fm][fn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[fm < NVA ? fm : 0], bf[fn],
@@ -383,21 +406,21 @@ __device__ __forceinline__ void pf_kloop(const PfSrc& dma, const PfSrc& nxt, con
         const int s3 = (rb + kt + 3) & 3;
         pf_dma<4, GATHER, !PF>(db, offs, sb, nk, s3, lds_base, wave);
         if constexpr (NV > 0) { rdb(kt, 1, 0, b1); rdb(kt, 1, 1, b1); }
-        mrow(0, a0, b0, zero_t);
+        mrow(std::integral_constant<int, 0>(), a0, b0, zero_t);
         fence();
         pf_dma<5, GATHER, !PF>(db, offs, sb, nk, s3, lds_base, wave);
         if constexpr (NV > 0) { rdb(kt, 1, 2, b1); rdb(kt, 1, 3, b1); }
-        mrow(1, a0, b0, zero_t);
+        mrow(std::integral_constant<int, 1>(), a0, b0, zero_t);
         fence();
         pf_dma<6, GATHER, !PF>(db, offs, sb, nk, s3, lds_base, wave);
         rda(kt, 1, 0, a1);
         rda(kt, 1, 1, a1);
-        mrow(2, a0, b0, zero_t);
+        mrow(std::integral_constant<int, 2>(), a0, b0, zero_t);
         fence();
         pf_dma<7, GATHER, !PF>(db, offs, sb, nk, s3, lds_base, wave);
         rda(kt, 1, 2, a1);
         rda(kt, 1, 3, a1);
-        mrow(3, a0, b0, zero_t);
+        mrow(std::integral_constant<int, 3>(), a0, b0, zero_t);
         fence();
     };
     // half 2 of iteration kt: stage kt + 1 landed (outstanding: stage kt + 2 and kt + 3) and stage
@@ -410,21 +433,21 @@ __device__ __forceinline__ void pf_kloop(const PfSrc& dma, const PfSrc& nxt, con
         const int s4 = (rb + kt) & 3;
         pf_dma<0, GATHER, !PF>(da, offs, sa, nk, s4, lds_base, wave);
         if constexpr (NV > 0) { rdb(kt + 1, 0, 0, b0); rdb(kt + 1, 0, 1, b0); }
-        mrow(0, a1, b1, F());
+        mrow(std::integral_constant<int, 0>(), a1, b1, F());
         fence();
         pf_dma<1, GATHER, !PF>(da, offs, sa, nk, s4, lds_base, wave);
         if constexpr (NV > 0) { rdb(kt + 1, 0, 2, b0); rdb(kt + 1, 0, 3, b0); }
-        mrow(1, a1, b1, F());
+        mrow(std::integral_constant<int, 1>(), a1, b1, F());
         fence();
         pf_dma<2, GATHER, !PF>(da, offs, sa, nk, s4, lds_base, wave);
         rda(kt + 1, 0, 0, a0);
         rda(kt + 1, 0, 1, a0);
-        mrow(2, a1, b1, F());
+        mrow(std::integral_constant<int, 2>(), a1, b1, F());
         fence();
         pf_dma<3, GATHER, !PF>(da, offs, sa, nk, s4, lds_base, wave);
         rda(kt + 1, 0, 2, a0);
         rda(kt + 1, 0, 3, a0);
-        mrow(3, a1, b1, F());
+        mrow(std::integral_constant<int, 3>(), a1, b1, F());
         fence();
     };
     // fragments without valid rows get no MFMAs: their accumulators are plain zeros
@@ -734,11 +757,194 @@ __device__ __forceinline__ void pf_epilogue(const GemmArgs& a, uint8_t* smem, v1
     }
 }
 
+// The deferred requant: a tile's activations stay in VGPRs after its epilogue has published the
+// row maxima, through the workgroup's whole next K loop; after that loop the row tile's exchange
+// has long completed, and the previous tile is requantised and stored before the current one is
+// published.  No workgroup waits for its row tile's other column tiles, so a late one (a slow
+// weight line, an HBM-bound tile of a small expert) costs nothing until it is a whole tile late.
+//
+// publish (after the K loop): SwiGLU from the accumulators into act, row maxima of |act| across
+// the lanes (DPP) and the two waves sharing the rows (LDS), one agent-scope atomicMax per (row,
+// tile), then one arrival on the row tile's counter once every maximum has completed.
+__device__ __forceinline__ void pf_publish(const GemmArgs& a, uint8_t* smem, v16i (&acc)[4][4], const PfTile& t,
+                                           const int par, float (&act)[4][2][16])
+{
+    const int tid = opaque((int)threadIdx.x), lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const EpiArgs& e = a.epi;
+    const CB_LDS float* xs_l = (const CB_LDS float*)((CB_LDS uint8_t*)smem + kPfSc + par * kPfScSlot);
+    const CB_LDS float* cs_l = xs_l + 256;
+    CB_LDS float* rm_l = (CB_LDS float*)((CB_LDS uint8_t*)smem + kPfRm);
+    const int h = lane >> 5, c = lane & 31;
+    float wsg[2], wsu[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        wsg[j] = cs_l[wn * 64 + j * 32 + c];
+        wsu[j] = cs_l[128 + wn * 64 + j * 32 + c];
+    }
+    // The activations are built in the accumulator registers the SwiGLU inputs free (the 128
+    // VGPRs they occupy during the next K loop are then not needed on top of this step's own), and
+    // moved to VGPRs at the end.
+    // lane (h, c) of fragment (fm, fn) holds rows (2 fm + wm) * 32 + 8 (r / 4) + 4 h + r % 4, column c
+#pragma unroll
+    for (int fm = 0; fm < 4; ++fm) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int row = (2 * fm + wm) * 32 + 8 * q + 4 * h;
+            const v4f xs4 = *(const CB_LDS v4f*)(xs_l + row);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    act[fm][j][4 * q + i] = to_agpr(swiglu((float)acc_read(acc[fm][j][4 * q + i]),
+                                                           (float)acc_read(acc[fm][j + 2][4 * q + i]), xs4[i], wsg[j], wsu[j]));
+        }
+    }
+    // |act| as u32 bit patterns, NaN counted as 0 (the reference's compare-based maximum ignores
+    // it); one fragment row at a time (16 values per lane), so that the maxima do not add 64
+    // registers to the 128 activations held here.  row_ror 1, 2, 4, 8 within each 16-lane row, then
+    // row_bcast:15 into rows 1 and 3: lanes 16..31 and 48..63 end with their half-wave's maximum.
+#pragma unroll
+    for (int fm = 0; fm < 4; ++fm) {
+        u32 m[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const u32 u0 = __float_as_uint(from_agpr(act[fm][0][r])) & 0x7fffffffu;
+            const u32 u1 = __float_as_uint(from_agpr(act[fm][1][r])) & 0x7fffffffu;
+            const u32 v0 = u0 > 0x7f800000u ? 0u : u0, v1 = u1 > 0x7f800000u ? 0u : u1;
+            m[r] = v0 > v1 ? v0 : v1;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) m[r] = umax_dpp<0x121, 0xF>(m[r]);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) m[r] = umax_dpp<0x122, 0xF>(m[r]);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) m[r] = umax_dpp<0x124, 0xF>(m[r]);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) m[r] = umax_dpp<0x128, 0xF>(m[r]);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) m[r] = umax_dpp<0x142, 0xA>(m[r]);
+        if (c == 16) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *(CB_LDS v4i*)(rm_l + wn * 256 + (2 * fm + wm) * 32 + 8 * q + 4 * h) =
+                    v4i{(int)m[4 * q], (int)m[4 * q + 1], (int)m[4 * q + 2], (int)m[4 * q + 3]};
+        }
+    }
+    __syncthreads();
+    if (tid < t.vrows) {
+        const u32 m0v = __float_as_uint(rm_l[tid]), m1v = __float_as_uint(rm_l[256 + tid]);
+        __hip_atomic_fetch_max(e.amax + t.m0 + tid, m0v > m1v ? m0v : m1v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // every row maximum of this tile has completed before the arrival (this also drains the next
+    // tile's first stages, so its loop starts without a vmcnt wait)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) __hip_atomic_fetch_add(e.arrive + t.mt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int fm = 0; fm < 4; ++fm)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) act[fm][j][r] = from_agpr(act[fm][j][r]);
+}
+
+// The pending requant of a workgroup's previous tile (has: one is pending).
+struct PfDefer {
+    float (&act)[4][2][16];  // its activations
+    const GemmArgs& a;
+    uint8_t* smem;
+    int nt;       // its column tile
+    u32 target;   // arrivals that complete a row tile's maxima
+    bool has;
+    PfTile t;     // its row tile
+
+    // The exchange wait (normally complete long since), 127 / amax of the tile's rows through LDS,
+    // then the requant and stores.  A wait that times out marks the tile for the fix-up launch and
+    // stores nothing.
+    __device__ __forceinline__ void run()
+    {
+        if (!has) return;
+        has = false;
+        const int tid = threadIdx.x;
+        const EpiArgs& e = a.epi;
+        CB_LDS u32* flag = (CB_LDS u32*)((CB_LDS uint8_t*)smem + kPfFlag);
+        if (tid == 0) {
+            int spins = 0;
+            u32 ok = 1;
+            while (__hip_atomic_load(e.arrive + t.mt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+                __builtin_amdgcn_s_sleep(8);
+                if (++spins > e.spin_limit) {
+                    ok = 0;
+                    break;
+                }
+            }
+            if (!ok) {
+                __hip_atomic_fetch_or(e.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(e.redo + t.mt * a.ntiles + nt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            *flag = ok;
+        }
+        __syncthreads();
+        if (__builtin_amdgcn_readfirstlane(*flag) == 0) return;
+        CB_LDS float* inv_l = (CB_LDS float*)((CB_LDS uint8_t*)smem + kPfInv);
+        float am = 0.0f;
+        if (tid < t.vrows) am = __uint_as_float(__hip_atomic_load(e.amax + t.m0 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        if (!(am > kFltMin)) am = kFltMin;
+        inv_l[tid] = 127.0f / am;
+        if (nt == 0 && tid < t.vrows) e.yq_scale[t.m0 + tid] = am * kInv127;
+        __syncthreads();
+        // y from column nt * 128 on: rows past the tile's valid rows lie past the resource's end
+        // (their offsets are at least vrows * H - nt * 128 while every valid one is below it, as
+        // nt * 128 + 128 <= H or the column check below removes the store)
+        const int64_t H = e.H;
+        const int64_t c0 = (int64_t)nt * 128;
+        const __amdgpu_buffer_rsrc_t yr =
+            make_rsrc(e.yq + (int64_t)t.m0 * H + c0, (uint32_t)((int64_t)(t.vrows < 256 ? t.vrows : 256) * H - c0));
+        const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), wm = wave >> 1, wn = wave & 1;
+        const int c = lane & 31, qi = c & 3, h = lane >> 5;
+        uint32_t ybase[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int cl = wn * 64 + j * 32 + (c & ~3);  // column within the tile's 128
+            ybase[j] = c0 + cl < H ? (uint32_t)((wm * 32 + 4 * h + qi) * H + cl) : 0x80000000u;
+        }
+        // lane (h, c) holds rows (2 fm + wm) * 32 + 8 q + 4 h + i of column c: rint16 of
+        // act * (127 / amax), a 4 x 4 byte transpose across each lane quad (lane qi ends with row
+        // + qi, columns (c & ~3) .. +3), one dword store per 32-column half
+#pragma unroll
+        for (int fm = 0; fm < 4; ++fm) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const v4f inv4 = *(const CB_LDS v4f*)(inv_l + (2 * fm + wm) * 32 + 8 * q + 4 * h);
+                const uint32_t roff = (uint32_t)((64 * fm + 8 * q) * H);  // rows below slice (0, 0)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    // clamp-and-narrow == saturating rint16; an all-zero row gives 0 * inf = NaN -> 0
+                    const u32 x = pack4_i8(rint16_h(act[fm][j][4 * q + 0] * inv4[0]), rint16_h(act[fm][j][4 * q + 1] * inv4[1]),
+                                           rint16_h(act[fm][j][4 * q + 2] * inv4[2]), rint16_h(act[fm][j][4 * q + 3] * inv4[3]));
+                    // step 1 swaps 16-bit halves with lane qi ^ 2, step 2 bytes with qi ^ 1
+                    const u32 pp = (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false);
+                    const u32 z = (qi & 2) ? __builtin_amdgcn_perm(x, pp, 0x07060302u) : __builtin_amdgcn_perm(pp, x, 0x05040100u);
+                    const u32 pz = (u32)__builtin_amdgcn_update_dpp(0, (int)z, 0xB1, 0xF, 0xF, false);
+                    const u32 y = (qi & 1) ? __builtin_amdgcn_perm(pz, z, 0x03070105u) : __builtin_amdgcn_perm(pz, z, 0x06020400u);
+                    __builtin_amdgcn_raw_buffer_store_b32((int)y, yr, ybase[j] + roff, 0, 0);
+                }
+            }
+        }
+    }
+};
+
 // Persistent GroupedMatmulSwigluQuant prefill kernel.  gridDim.x workgroups, at most one per CU,
 // all resident together (the host checks the occupancy).  Exchange group: the row maxima of
 // row tile mt are final once its ntl column tiles have counted at arrive[mt].  GATHER: activation rows
 // through the row index.
-template <bool GATHER>
+// DEFER: each tile's requant waits until the workgroup's next K loop is done (PfDefer); needs the
+// K loop that carries the next tile's prologue (K of at least kPfDeferMinStages stages).
+constexpr int kPfDeferMinStages = 4;
+
+template <bool GATHER, bool DEFER>
 __global__ __launch_bounds__(256, 1) void gmsq_prefill_kernel(const GemmArgs a)
 {
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
@@ -754,10 +960,17 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_kernel(const GemmArgs a)
     uint32_t a_rd[4][2], b_rd[4];
     pf_read_offsets(wm, wn, lane, a_rd, b_rd);
     const int nk = __builtin_amdgcn_readfirstlane((int)((a.K + PfCfg::BK - 1) / PfCfg::BK));
-    const PfOffs offs = pf_offsets<GATHER>(a, pl.nt, wave, lane);
+    PfOffs offs = pf_offsets<GATHER>(a, wave, lane);
 
     int q = pl.slot;
     if (q >= rounds) return;
+    // Round r of a slot gives its workgroup of column position pl.nt the column tile
+    // (pl.nt + r) % ntl: every workgroup takes each column tile in turn.  The tiles whose weight
+    // lines sit at slow HBM addresses (a fixed maximum read rate: two of the sixteen column tiles
+    // of a 4 KB weight row) then fall to a different workgroup every round, and with the requant
+    // carried by the next K loop a round's late tile is absorbed instead of setting every round's
+    // pace.
+    auto nt_of = [&](int qq) { return (pl.nt + qq / pl.slots) % ntl; };
     // this tile's scales into LDS slot par (the wait for their loads also waits for the prologue)
     auto put_scales = [&](const PfScales& v, int par) {
         CB_LDS float* sl = (CB_LDS float*)((CB_LDS uint8_t*)smem + kPfSc + par * kPfScSlot);
@@ -771,23 +984,30 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_kernel(const GemmArgs a)
     // 3.5 stages then all lie in the last 4 iterations)
     const bool pf = nk >= 4;
     if (cur_t.mt >= 0) {
-        cur = pf_src<GATHER>(a, cur_t.g, cur_t.m0, cur_t.vrows, wave, lane);
+        cur = pf_src<GATHER>(a, cur_t.g, cur_t.m0, cur_t.vrows, nt_of(q), wave, lane);
         pf_prologue<GATHER>(cur, offs, nk, smem, wave);
-        put_scales(pf_scales(a, cur_t, pl.nt), par);
+        put_scales(pf_scales(a, cur_t, nt_of(q)), par);
     }
     bool first = true;
+    float act[4][2][16];  // DEFER: the pending tile's activations
+    PfDefer def{act, a, smem, 0, target, false, cur_t};
     for (; q < rounds; q += pl.slots) {
         // the next round's tile of this workgroup: its plan and scales are prepared now, and its
         // first stages are fetched by this tile's K loop past K
+        // opaque: the DMA offsets derived from these (every stage of every loop variant) are
+        // computed per tile, not hoisted out of the tile loop and spilled
+        offs.a0 = opaque(offs.a0);
+        offs.b0 = opaque(offs.b0);
         const int qn = q + pl.slots;
         const PfTile nxt_t = pf_round_tile(a.gt, tab, ord, pl.RT, qn, pl.rt);
         if (cur_t.mt < 0) {
             // past the last row tile of its kind (no exchange: the counters are per row tile)
+            if (DEFER) def.run();
             if (nxt_t.mt >= 0) {
                 __syncthreads();
-                cur = pf_src<GATHER>(a, nxt_t.g, nxt_t.m0, nxt_t.vrows, wave, opaque(lane));
+                cur = pf_src<GATHER>(a, nxt_t.g, nxt_t.m0, nxt_t.vrows, nt_of(qn), wave, opaque(lane));
                 pf_prologue<GATHER>(cur, offs, nk, smem, wave);
-                put_scales(pf_scales(a, nxt_t, pl.nt), par);
+                put_scales(pf_scales(a, nxt_t, nt_of(qn)), par);
                 rb = 0;
                 first = true;
             }
@@ -797,8 +1017,8 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_kernel(const GemmArgs a)
         PfSrc nxt;
         PfScales nsc;
         if (nxt_t.mt >= 0) {
-            nxt = pf_src<GATHER>(a, nxt_t.g, nxt_t.m0, nxt_t.vrows, wave, opaque(lane));
-            nsc = pf_scales(a, nxt_t, pl.nt);
+            nxt = pf_src<GATHER>(a, nxt_t.g, nxt_t.m0, nxt_t.vrows, nt_of(qn), wave, opaque(lane));
+            nsc = pf_scales(a, nxt_t, nt_of(qn));
         } else {
             nxt = pf_dead(a);
         }
@@ -812,7 +1032,19 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_kernel(const GemmArgs a)
             rb = 0;
             first = true;
         }
-        if (pf) {
+        if constexpr (DEFER) {
+            // pf holds (nk >= kPfDeferMinStages)
+            if (nv >= 4) pf_kloop<4, true, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+            else if (nv == 3) pf_kloop<3, true, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+            else if (nv == 2) pf_kloop<2, true, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+            else if (nv == 1) pf_kloop<1, true, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+            else pf_kloop<0, true, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
+            def.run();
+            pf_publish(a, smem, acc, cur_t, par, act);
+            def.has = true;
+            def.t = cur_t;
+            def.nt = nt_of(q);
+        } else if (pf) {
             if (nv >= 4) pf_kloop<4, true, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
             else if (nv == 3) pf_kloop<3, true, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
             else if (nv == 2) pf_kloop<2, true, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
@@ -825,7 +1057,7 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_kernel(const GemmArgs a)
             else if (nv == 1) pf_kloop<1, false, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
             else pf_kloop<0, false, GATHER>(cur, nxt, offs, nk, rb, smem, a_rd, b_rd, acc, wave, first);
         }
-        pf_epilogue<false>(a, smem, acc, cur_t, pl.nt, par, cur_t.mt, target, cur_t.mt * ntl + pl.nt);
+        if constexpr (!DEFER) pf_epilogue<false>(a, smem, acc, cur_t, nt_of(q), par, cur_t.mt, target, cur_t.mt * ntl + nt_of(q));
         if (nxt_t.mt >= 0) put_scales(nsc, par ^ 1);
         // every wave is past its LDS reads of this epilogue (and the next scales are written)
         // before the next tile's epilogue
@@ -836,6 +1068,7 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_kernel(const GemmArgs a)
         first = false;
         cur_t = nxt_t;
     }
+    if (DEFER) def.run();
 }
 
 // Fix-up launch: recomputes the tiles whose exchange wait timed out (redo[mt * ntl + nt] != 0),
@@ -860,8 +1093,8 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_fixup_kernel(const GemmAr
             continue;
         const int nt = t % ntl;
         const PfTile tl = pf_tile_at(a.gt, t / ntl);
-        const PfOffs offs = pf_offsets<GATHER>(a, nt, wave, opaque(lane));
-        const PfSrc cur = pf_src<GATHER>(a, tl.g, tl.m0, tl.vrows, wave, opaque(lane));
+        const PfOffs offs = pf_offsets<GATHER>(a, wave, opaque(lane));
+        const PfSrc cur = pf_src<GATHER>(a, tl.g, tl.m0, tl.vrows, nt, wave, opaque(lane));
         __syncthreads();
         pf_prologue<GATHER>(cur, offs, nk, smem, wave);
         {

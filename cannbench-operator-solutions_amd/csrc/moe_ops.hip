@@ -283,7 +283,11 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
         const int cus = device_cus();
         const int grid = (ntl == 16 && cus >= 256) ? 256 : (cus / ntl) * ntl;
         const bool gather = row_index != nullptr;
-        const void* main_k = gather ? (const void*)gmsq_prefill_kernel<true> : (const void*)gmsq_prefill_kernel<false>;
+        const bool defer = (K + PfCfg::BK - 1) / PfCfg::BK >= kPfDeferMinStages;
+        const void* main_k = gather ? (defer ? (const void*)gmsq_prefill_kernel<true, true>
+                                             : (const void*)gmsq_prefill_kernel<true, false>)
+                                    : (defer ? (const void*)gmsq_prefill_kernel<false, true>
+                                             : (const void*)gmsq_prefill_kernel<false, false>);
         const void* fix_k =
             gather ? (const void*)gmsq_prefill_fixup_kernel<true> : (const void*)gmsq_prefill_fixup_kernel<false>;
         int resident = 0;
@@ -298,8 +302,8 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
             const dim3 fix_grid((unsigned)(tiles < 256 ? tiles : 256));
             {
                 TimedLaunch timed(st);
-                if (gather) hipLaunchKernelGGL(gmsq_prefill_kernel<true>, dim3((unsigned)grid), dim3(256), kPfLds, st, a);
-                else hipLaunchKernelGGL(gmsq_prefill_kernel<false>, dim3((unsigned)grid), dim3(256), kPfLds, st, a);
+                void* args[] = {(void*)&a};
+                (void)hipLaunchKernel(main_k, dim3((unsigned)grid), dim3(256), args, kPfLds, st);  // checked below
             }
             if (gather) hipLaunchKernelGGL(gmsq_prefill_fixup_kernel<true>, fix_grid, dim3(256), kPfLds, st, a);
             else hipLaunchKernelGGL(gmsq_prefill_fixup_kernel<false>, fix_grid, dim3(256), kPfLds, st, a);
