@@ -178,17 +178,21 @@ __device__ __forceinline__ PfPlace pf_place(int ntl, int grid, int b)
 {
     PfPlace p;
     if (ntl == 16 && grid == 256) {
-        // Workgroup b is dispatched to XCD b % 8.  Slot s = XCD s: its 32 workgroups hold the
-        // slot's 2 row tiles x all 16 column tiles, so an activation slab is fetched into one L2
-        // only and a round's exchange stays inside one XCD.  (Measured against 4 row tiles x 8
-        // column tiles per XCD on XCD pairs: Zipf -1%, full tiles -1.5%, single-tile experts -5%
-        // of the time; against 1 row tile per slot: Zipf -1%.)
+        // Workgroup b is dispatched to XCD b % 8.  Slot s = the XCD pair (2 s, 2 s + 1): its 64
+        // workgroups hold the slot's 4 row tiles x all 16 column tiles, column tiles 0-7 on the
+        // even XCD and 8-15 on the odd one (before the per-round rotation).  Each XCD then streams
+        // half of a heavy expert's weight for 4 row tiles, where one XCD per 2 row tiles streamed
+        // all of it: the weight bytes fetched from HBM per heavy row tile halve, for twice the
+        // activation fetches (each row tile's activation slab goes to two L2s).  Measured, same
+        // box, interleaved: Zipf 4.04-4.07 ms against 4.07-4.12 with one XCD per 2 row tiles x 16
+        // column tiles; XCD quads (8 row tiles x 4 column tiles per XCD) 4.08-4.10, all 8 XCDs
+        // (16 x 2) 4.18-4.20.
         const int x = b & 7, j = b >> 3;
-        p.slot = x;
-        p.rt = j >> 4;
-        p.nt = j & 15;
-        p.slots = 8;
-        p.RT = 2;
+        p.slot = x >> 1;
+        p.rt = j >> 3;
+        p.nt = 8 * (x & 1) + (j & 7);
+        p.slots = 4;
+        p.RT = 4;
     } else {
         p.slot = b / ntl;
         p.rt = 0;
