@@ -470,7 +470,7 @@ def main():
         out["copy"] = {"value": round(c["gbs"], 1), "unit": "GB/s", "ms_per_step": round(c["ms"], 4),
                        "bytes_read": c["bytes_read"], "bytes_written": c["bytes_written"]}
     if out.get("roofline") is not None:
-        out["roofline"]["traffic"] = traffic_from_profiles("prefill_gemm", "cb::gmsq_prefill_kernel<false>(")
+        out["roofline"]["traffic"] = traffic_from_profiles("prefill_gemm", "cb::gmsq_prefill_kernel<false, true>(")
     if "decode" in out:
         out["decode"]["roofline"]["traffic"] = traffic_from_profiles("decode_gemm", "cb::gmsq_decode_kernel(")
         out["down_proj"]["roofline"]["traffic"] = traffic_from_profiles("down_proj_gemm", "cb::skinny_kernel<1")
