@@ -409,8 +409,10 @@ def cpu_baseline(d, budget_s=12.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=10,
+                    help="untimed calls per workload first: the clock settles at the board power limit over "
+                         "the first 5-6 prefill calls (4.7-5.0 ms, then 4.1-4.2 ms)")
     ap.add_argument("--only", default="prefill,gather,down_prefill,decode,ardq,qmm,routing,gmm,vendor",
                     help="comma list of prefill, gather and down_prefill (need prefill), decode, ardq, qmm, "
                          "routing, gmm, vendor, copy")
