@@ -141,6 +141,8 @@ GMSQ_CASES = [
     ([640], 256, 1024),                        # all rows in one expert, E = 1
     ([100, 300, 37], 400, 896),                # fused persistent path: K tail (400 = 3 x 128 + 16), H = 448 (last column tile half full)
     ([260, 0, 33], 7184, 4128),                # fused path: K = 7168 + 16, H = 2064 (17 column tiles, the last 16 columns wide)
+    ([100, 300, 37], 192, 1024),               # fused path, K of 3 stages: lock-step requant (no stage stream across tiles)
+    ([70, 0, 513, 40], 128, 4096),             # the same at 16 column tiles (XCD-pair slots), K of 2 stages
     ([6, 11], 80, 48),                         # K % 16 == 0, H = 24 not a multiple of 16 -> generic
     ([4, 4], 40, 64),                          # K % 16 != 0 -> generic
 ]
