@@ -43,9 +43,6 @@ struct Vec16 {
     uint16_t v[VEC];
 };
 
-#ifndef CB_ROW_NT
-#define CB_ROW_NT 1
-#endif
 typedef int rv4i __attribute__((ext_vector_type(4)));
 
 template <int VEC>
@@ -54,8 +51,7 @@ __device__ __forceinline__ Vec16<VEC> ldv(const uint16_t* p)
     Vec16<VEC> r;
     if constexpr (VEC == 8) {
         // row data is read exactly once: nontemporal loads keep it from displacing other lines
-        const rv4i q = CB_ROW_NT ? __builtin_nontemporal_load(reinterpret_cast<const rv4i*>(p))
-                                 : *reinterpret_cast<const rv4i*>(p);
+        const rv4i q = __builtin_nontemporal_load(reinterpret_cast<const rv4i*>(p));
         __builtin_memcpy(r.v, &q, 16);
     } else {
 #pragma unroll
@@ -70,8 +66,7 @@ __device__ __forceinline__ void stv(uint16_t* p, const Vec16<VEC>& r)
     if constexpr (VEC == 8) {
         rv4i q;
         __builtin_memcpy(&q, r.v, 16);
-        if (CB_ROW_NT) __builtin_nontemporal_store(q, reinterpret_cast<rv4i*>(p));
-        else *reinterpret_cast<rv4i*>(p) = q;
+        __builtin_nontemporal_store(q, reinterpret_cast<rv4i*>(p));
     } else {
 #pragma unroll
         for (int j = 0; j < VEC; ++j) p[j] = r.v[j];
@@ -86,8 +81,7 @@ __device__ __forceinline__ void sty8(int8_t* p, const int* q)
         rv2i w;
         w[0] = (int)pack4_i8(q[0], q[1], q[2], q[3]);
         w[1] = (int)pack4_i8(q[4], q[5], q[6], q[7]);
-        if (CB_ROW_NT) __builtin_nontemporal_store(w, reinterpret_cast<rv2i*>(p));
-        else *reinterpret_cast<rv2i*>(p) = w;
+        __builtin_nontemporal_store(w, reinterpret_cast<rv2i*>(p));
     } else {
 #pragma unroll
         for (int j = 0; j < VEC; ++j) p[j] = (int8_t)q[j];
@@ -285,13 +279,11 @@ struct RowPlan {
     int nv;
 };
 
-#ifndef CB_ROW_MAX_THREADS
-#define CB_ROW_MAX_THREADS 512
-#endif
+constexpr int kRowMaxThreads = 512;
 
 // Row split: VEC elements per access (8 when rows are 16-byte aligned), `threads` a multiple of 64,
 // NV accesses per thread.  Vector path: the (threads, NV <= 8) pair with the fewest idle slots,
-// preferring wider workgroups up to CB_ROW_MAX_THREADS.  Scalar path: powers of two.
+// preferring wider workgroups up to kRowMaxThreads.  Scalar path: powers of two.
 static RowPlan plan_row(int64_t n, bool aligned16)
 {
     RowPlan p;
@@ -305,7 +297,7 @@ static RowPlan plan_row(int64_t n, bool aligned16)
             if (nv > 8) continue;
             const int64_t waste = t * nv - nvec;
             const bool better = waste < best_waste ||
-                                (waste == best_waste && t <= CB_ROW_MAX_THREADS && (best_t > CB_ROW_MAX_THREADS || t > best_t));
+                                (waste == best_waste && t <= kRowMaxThreads && (best_t > kRowMaxThreads || t > best_t));
             if (better) {
                 best_waste = waste;
                 best_t = t;
