@@ -174,12 +174,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 
 // Weight streams are read once: nontemporal loads (aux bit "nt") keep them from displacing the
 // activations and scales in L2.
-#ifndef CB_STREAM_AUX
-#define CB_STREAM_AUX 2
-#endif
+constexpr int kStreamAux = 2;
 __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff)
 {
-    const v4i v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, CB_STREAM_AUX);
+    const v4i v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, kStreamAux);
     return make_uint4((u32)v[0], (u32)v[1], (u32)v[2], (u32)v[3]);
 }
 

@@ -25,10 +25,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 
 constexpr int kGmmMaxExperts = 64;  // GMM_MAX_E (grouped_matmul_launch.h)
-#ifndef CB_GMM_BK
-#define CB_GMM_BK 32
-#endif
-constexpr int GF_BK = CB_GMM_BK;
+constexpr int GF_BK = 32;
 // elements per LDS row (BK + 8: 80 B at BK 32): a 16-lane b128 read phase hits 16 distinct bank groups
 constexpr int GF_PITCH = GF_BK + 8;
 constexpr int GF_KCH = GF_BK / 8;  // 16-byte chunks per row and stage

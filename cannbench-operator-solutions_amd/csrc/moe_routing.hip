@@ -474,9 +474,7 @@ __device__ __forceinline__ float ld_x(const void* x, int64_t i)
 
 constexpr int kDqsqMaxPerThread = 16;
 // values per thread of the vectorised DequantSwigluQuant row (sets its threads per row)
-#ifndef CB_DQSQ_EPT
-#define CB_DQSQ_EPT 4
-#endif
+constexpr int kDqsqEpt = 4;
 
 template <int XDT>
 __device__ __forceinline__ float dqsq_elem(const void* x, int64_t base, int64_t H, int64_t j, const float* ws,
@@ -933,8 +931,8 @@ extern "C" int cb_dequant_swiglu_quant(const void* x, int x_dtype, int64_t M, in
     const int NVcap = 16 / V;  // register budget: 16 values per thread
     if (H % V == 0 && aligned(x, 16) && aligned(y, 8) && H / V <= (int64_t)NVcap * 512) {
         const int64_t nvh = H / V;
-        // CB_DQSQ_EPT values per thread (more threads per row measured faster), more for long rows
-        int NVmax = (CB_DQSQ_EPT / V) < 1 ? 1 : CB_DQSQ_EPT / V;
+        // kDqsqEpt values per thread (more threads per row measured faster), more for long rows
+        int NVmax = (kDqsqEpt / V) < 1 ? 1 : kDqsqEpt / V;
         while (NVmax < NVcap && nvh > (int64_t)NVmax * 512) NVmax *= 2;
         // threads that cover the row in NVmax passes
         int threads = (int)(((nvh + NVmax - 1) / NVmax + 63) / 64 * 64);
