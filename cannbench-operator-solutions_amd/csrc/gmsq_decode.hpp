@@ -191,7 +191,8 @@ __device__ __forceinline__ void decode_finish(const GemmArgs& a, const int g, co
                                               const float (&act)[2][16])
 {
     float am[2];
-    if (decode_gather(a, r0, r1, am)) {
+    // a negative poll limit (test hook) gives up at once
+    if (a.epi.spin_limit >= 0 && decode_gather(a, r0, r1, am)) {
         decode_tile_quant(a, ct, r0, r1, act, am);
     } else if ((threadIdx.x & 63) == 0) {
         __hip_atomic_fetch_or(a.epi.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

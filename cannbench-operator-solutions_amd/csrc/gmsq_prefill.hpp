@@ -696,8 +696,8 @@ __device__ __forceinline__ void pf_epilogue(const GemmArgs& a, uint8_t* smem, v1
         if (tid == 0) {
             __hip_atomic_fetch_add(e.arrive + arr_idx, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             int spins = 0;
-            u32 ok = 1;
-            while (__hip_atomic_load(e.arrive + arr_idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < arr_target) {
+            u32 ok = e.spin_limit < 0 ? 0u : 1u;  // a negative limit (test hook): give up at once
+            while (ok && __hip_atomic_load(e.arrive + arr_idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < arr_target) {
                 __builtin_amdgcn_s_sleep(8);
                 if (++spins > e.spin_limit) {
                     ok = 0;
@@ -876,8 +876,8 @@ struct PfDefer {
         CB_LDS u32* flag = (CB_LDS u32*)((CB_LDS uint8_t*)smem + kPfFlag);
         if (tid == 0) {
             int spins = 0;
-            u32 ok = 1;
-            while (__hip_atomic_load(e.arrive + t.mt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            u32 ok = e.spin_limit < 0 ? 0u : 1u;  // a negative limit (test hook): give up at once
+            while (ok && __hip_atomic_load(e.arrive + t.mt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
                 __builtin_amdgcn_s_sleep(8);
                 if (++spins > e.spin_limit) {
                     ok = 0;

@@ -269,7 +269,7 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
     a.epi.redo = (u32*)(wsb + ws.redo_off);
     a.epi.yq = y;
     a.epi.yq_scale = y_scale;
-    a.epi.spin_limit = g_overrides.exchange_spin_limit > 0 ? g_overrides.exchange_spin_limit : kExchangeSpins;
+    a.epi.spin_limit = g_overrides.exchange_spin_limit != 0 ? g_overrides.exchange_spin_limit : kExchangeSpins;
     build_group_table(a.gt, group_list, E, 256);
     // row maxima, arrival counters, the status word and the fix-up marks are contiguous: one fill
     // clears what this call's launches use

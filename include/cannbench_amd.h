@@ -193,7 +193,8 @@ int cb_grouped_matmul_swiglu_quant_noalloc(const int8_t* x, const int8_t* weight
  *                        persistent launch off.
  *   exchange_spin_limit  polls of the GroupedMatmulSwigluQuant row-maximum exchange before a tile
  *                        gives up and leaves its output to the fix-up launch (default 2^20, about
- *                        2 s); a small value exercises the fix-up path.
+ *                        2 s); a small value exercises the fix-up path, a negative one makes every
+ *                        wait give up at once (the fix-up launch then writes every tile).
  *   gmm_tile             128 forces the 128 x 128 GroupedMatmul kernel for every fp16/bf16 shape.
  */
 void cb_set_test_overrides(int persistent_grid, int exchange_spin_limit, int gmm_tile);

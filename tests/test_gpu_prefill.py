@@ -64,19 +64,24 @@ def _run_raw(cb, x, w, ws, xs, gl):
     return y, ys, wsp
 
 
+@pytest.mark.parametrize("limit", [1, -1])
 @pytest.mark.parametrize("counts,K,N", [
     ([300, 0, 700, 45, 1000], 512, 4096),   # prefill, 16 column tiles: the 256-workgroup grid, 4 row tiles per round
     ([260, 33, 513], 384, 1024),            # prefill, 4 column tiles: one row tile per exchange group
+    ([300, 0, 513], 128, 4096),             # prefill, K of 2 stages: the lock-step requant
     ([5, 0, 17, 32, 1, 9] * 8, 448, 4096),  # decode: at most 32 rows per expert, 16 column tiles
     ([3, 31, 0, 12], 320, 1056),            # decode: 5 column tiles, the last one partial
 ])
-def test_exchange_timeout_fixup(cb, orc, overrides, counts, K, N):
+def test_exchange_timeout_fixup(cb, orc, overrides, counts, K, N, limit):
+    """limit 1: one poll, so tiles whose partners have not all arrived give up; limit -1: every
+    wait gives up at once, so the fix-up launch writes every tile.  Either way the outputs equal the
+    normal run's."""
     x, w, ws, xs, gl = _inputs(counts, K, N, sum(counts) + K)
     M, E = sum(counts), len(counts)
     y0, ys0, wsp0 = _run_raw(cb, x, w, ws, xs, gl)
     torch.cuda.synchronize()
     assert _status(cb, wsp0, M, N, E) == 0
-    overrides(exchange_spin_limit=1)  # one poll: tiles whose partners have not all arrived give up
+    overrides(exchange_spin_limit=limit)
     y1, ys1, wsp1 = _run_raw(cb, x, w, ws, xs, gl)
     torch.cuda.synchronize()
     gave_up = _status(cb, wsp1, M, N, E)
@@ -87,16 +92,17 @@ def test_exchange_timeout_fixup(cb, orc, overrides, counts, K, N):
     np.testing.assert_allclose(ys1.cpu().numpy(), ysr, rtol=1e-5)
     d = np.abs(y1.cpu().numpy().astype(np.int32) - yr.astype(np.int32))
     assert d.max() <= 1
-    # with one poll some tile gives up in practice; the status word says so (never required for
-    # correctness, which the comparisons above check either way)
-    assert gave_up in (0, 1)
+    # with one poll a tile may or may not give up (the status word says which; correctness, checked
+    # above, holds either way); with no poll every tile gives up
+    assert gave_up == 1 if limit < 0 else gave_up in (0, 1)
 
 
+@pytest.mark.parametrize("limit", [1, -1])
 @pytest.mark.parametrize("counts,K,N,T", [
     ([300, 0, 700, 45, 1000], 512, 4096, 900),   # prefill kernel with gathered rows
     ([5, 0, 17, 32, 1, 9] * 8, 448, 4096, 200),  # decode kernel with gathered rows
 ])
-def test_gather_exchange_timeout_fixup(cb, overrides, counts, K, N, T):
+def test_gather_exchange_timeout_fixup(cb, overrides, counts, K, N, T, limit):
     """The gathered variants under a one-poll exchange limit: the fix-up launches recompute the
     tiles that gave up through the same row index, so the outputs equal the normal run's."""
     g = cpu_gen(T + K)
@@ -109,7 +115,7 @@ def test_gather_exchange_timeout_fixup(cb, overrides, counts, K, N, T):
     gl = np.cumsum(counts).tolist()
     y0, ys0 = cb.grouped_matmul_swiglu_quant_gather(x, idx, w, ws, xs, gl)
     torch.cuda.synchronize()
-    overrides(exchange_spin_limit=1)
+    overrides(exchange_spin_limit=limit)
     y1, ys1 = cb.grouped_matmul_swiglu_quant_gather(x, idx, w, ws, xs, gl)
     torch.cuda.synchronize()
     overrides()
