@@ -150,7 +150,11 @@ __device__ __forceinline__ bool decode_gather(const GemmArgs& a, const int r0, c
             all = all && ok;
         }
         if (__builtin_amdgcn_ballot_w64(!all) == 0) return true;  // all 64 lanes' rows are final
-        if (spins >= a.epi.spin_limit) return false;
+        // give up after spin_limit polls, or once any wait of the call has given up (the status
+        // word: the rest of the call then leaves its tiles to the fix-up launch at once)
+        if (spins >= a.epi.spin_limit ||
+            ((spins & 255) == 255 && __hip_atomic_load(a.epi.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u))
+            return false;
         __builtin_amdgcn_s_sleep(4);
     }
 }

@@ -590,6 +590,23 @@ __device__ __forceinline__ int rint16_h(float v)
     return i;
 }
 
+// The exchange wait of one thread: poll the counter until it reaches target, at most spin_limit
+// times (a negative limit, the test hook, gives up at once).  Once any wait of the call has given
+// up (the status word is set, e.g. because CUs held by other work keep part of the grid from
+// running), every later wait gives up at once too, so the call stalls for one wait at most and
+// the fix-up launch computes the rest.  Returns 0 when it gave up.
+__device__ __forceinline__ u32 pf_wait(const EpiArgs& e, u32* counter, const u32 target)
+{
+    if (e.spin_limit < 0) return 0u;
+    for (int spins = 0; __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target; ++spins) {
+        if (spins >= e.spin_limit ||
+            ((spins & 255) == 0 && __hip_atomic_load(e.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u))
+            return 0u;
+        __builtin_amdgcn_s_sleep(8);
+    }
+    return 1u;
+}
+
 // One persistent GMSQ tile after its K loop: everything from the SwiGLU to the int8 stores.
 // Returns false when the exchange wait timed out (the tile stored nothing and is marked for the
 // fix-up launch).
@@ -695,15 +712,7 @@ __device__ __forceinline__ void pf_epilogue(const GemmArgs& a, uint8_t* smem, v1
         __syncthreads();
         if (tid == 0) {
             __hip_atomic_fetch_add(e.arrive + arr_idx, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            int spins = 0;
-            u32 ok = e.spin_limit < 0 ? 0u : 1u;  // a negative limit (test hook): give up at once
-            while (ok && __hip_atomic_load(e.arrive + arr_idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < arr_target) {
-                __builtin_amdgcn_s_sleep(8);
-                if (++spins > e.spin_limit) {
-                    ok = 0;
-                    break;
-                }
-            }
+            const u32 ok = pf_wait(e, e.arrive + arr_idx, arr_target);
             if (!ok) {
                 // this tile's y waits for the fix-up launch
                 __hip_atomic_fetch_or(e.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -875,15 +884,7 @@ struct PfDefer {
         const EpiArgs& e = a.epi;
         CB_LDS u32* flag = (CB_LDS u32*)((CB_LDS uint8_t*)smem + kPfFlag);
         if (tid == 0) {
-            int spins = 0;
-            u32 ok = e.spin_limit < 0 ? 0u : 1u;  // a negative limit (test hook): give up at once
-            while (ok && __hip_atomic_load(e.arrive + t.mt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-                __builtin_amdgcn_s_sleep(8);
-                if (++spins > e.spin_limit) {
-                    ok = 0;
-                    break;
-                }
-            }
+            const u32 ok = pf_wait(e, e.arrive + t.mt, target);
             if (!ok) {
                 __hip_atomic_fetch_or(e.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(e.redo + t.mt * a.ntiles + nt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
