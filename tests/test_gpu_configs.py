@@ -113,6 +113,23 @@ def test_gmsq_prefill_config4(cb, orc, prefill):
             check(g, max(s + 700, last - 256), e)
 
 
+def test_gmsq_prefill_config4_gathered(cb, prefill):
+    """The MoE flow at full config-4 size: activation rows gathered through a row index (a seeded
+    permutation of the 131072 rows, as MoeReRouting would produce) equal the operator on the
+    explicitly gathered x[idx], x_scale[idx], bit for bit (y and y_scale)."""
+    d = prefill
+    M = d["x"].shape[0]
+    idx = torch.from_numpy(np.random.default_rng(7).permutation(M).astype(np.int32)).to(d["x"].device)
+    y1, ys1 = cb.grouped_matmul_swiglu_quant_gather(d["x"], idx, d["weight"], d["weight_scale"], d["x_scale"],
+                                                    d["group_list"])
+    xg, xsg = d["x"][idx.long()], d["x_scale"][idx.long()]
+    y2, ys2 = cb.grouped_matmul_swiglu_quant(xg, d["weight"], d["weight_scale"], xsg, d["group_list"])
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2), "gathered int8 output differs from the explicit gather"
+    assert torch.equal(ys1, ys2), "gathered scales differ from the explicit gather"
+    del y1, y2, xg
+
+
 def test_gmsq_prefill_every_row_vs_int32_core(cb, prefill):
     """Every row of the prefill config: the operator (persistent GEMM with the cross-tile row-max
     exchange) against the exact int32 core plus a plain torch fp32 epilogue on the device (the
