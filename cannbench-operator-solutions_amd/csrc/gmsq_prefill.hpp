@@ -973,8 +973,8 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_kernel(const GemmArgs a)
     // (pl.nt + r) % ntl: every workgroup takes each column tile in turn.  The tiles whose weight
     // lines sit at slow HBM addresses (a fixed maximum read rate: two of the sixteen column tiles
     // of a 4 KB weight row) then fall to a different workgroup every round, and with the requant
-    // carried by the next K loop a round's late tile is absorbed instead of setting every round's
-    // pace.
+    // deferred past the next K loop (DEFER) a round's late tile is absorbed instead of setting
+    // every round's pace.
     auto nt_of = [&](int qq) { return (pl.nt + qq / pl.slots) % ntl; };
     // this tile's scales into LDS slot par (the wait for their loads also waits for the prologue)
     auto put_scales = [&](const PfScales& v, int par) {
@@ -997,12 +997,12 @@ __global__ __launch_bounds__(256, 1) void gmsq_prefill_kernel(const GemmArgs a)
     float act[4][2][16];  // DEFER: the pending tile's activations
     PfDefer def{act, a, smem, 0, target, false, cur_t};
     for (; q < rounds; q += pl.slots) {
-        // the next round's tile of this workgroup: its plan and scales are prepared now, and its
-        // first stages are fetched by this tile's K loop past K
         // opaque: the DMA offsets derived from these (every stage of every loop variant) are
         // computed per tile, not hoisted out of the tile loop and spilled
         offs.a0 = opaque(offs.a0);
         offs.b0 = opaque(offs.b0);
+        // the next round's tile of this workgroup: its plan and scales are prepared now, and its
+        // first stages are fetched by this tile's K loop past K
         const int qn = q + pl.slots;
         const PfTile nxt_t = pf_round_tile(a.gt, tab, ord, pl.RT, qn, pl.rt);
         if (cur_t.mt < 0) {
