@@ -204,35 +204,23 @@ __device__ __forceinline__ void decode_finish(const GemmArgs& a, const int g, co
     }
 }
 
-// Persistent decode kernel with dynamic tile order.  The tiles (expert g, column tile ct) form 8
-// lists, one per XCD (workgroup b runs on XCD b % 8): XCD x takes the experts g = x / 2 + 4 i and
-// the column half x % 2 (8 adjacent 128-act-column tiles: 1 KB runs of every weight row), in
-// expert order; its workgroups draw tiles from the list with an atomic ticket, so a faster CU
-// simply takes more tiles.  (With other tile or expert counts there is one list in natural
-// order.)  An expert's column tiles are drawn together, so they finish together: each tile
-// publishes its row maxima and arrives at arrive[g] as soon as its product is done, and its
-// requant is deferred until the workgroup's next tile is done, by which time the expert's other
-// column tiles have normally published; the deferred activations wait in LDS.  No tile waits
-// before publishing, so every drawn tile publishes and the waits cannot form a cycle.
-__global__ __launch_bounds__(256, 2) void gmsq_decode_kernel(const GemmArgs a, const int xcd_lists)
+// Persistent decode kernel with dynamic tile order.  The tiles (expert g, 128-act-column tile ct)
+// are numbered in expert order, t = g * ntiles + ct, and the workgroups draw them with one atomic
+// ticket, so a faster CU simply takes more tiles.  (Measured: one list in expert order beats 8
+// per-XCD lists, each holding a quarter of the experts and half of the columns.)  An expert's
+// column tiles are drawn together, so they finish together: each tile publishes its row maxima
+// into the self-validating slots as soon as its product is done, and its requant is deferred until
+// the workgroup's next tile is done, by which time the expert's other column tiles have normally
+// published; the deferred activations wait in LDS.  No tile waits before publishing, so every
+// drawn tile publishes and the waits cannot form a cycle.
+__global__ __launch_bounds__(256, 2) void gmsq_decode_kernel(const GemmArgs a)
 {
     __shared__ int red[3][4][16][64];      // partial sums handed to the wave that owns them (48 KiB)
     __shared__ float park[4][4][8][2][16]; // the deferred tile's activations (lanes c < 8; 16 KiB)
     __shared__ u32 next_t;
     const int ntl = a.ntiles;
-    const int E = a.gt.n_groups;
-    const int list = xcd_lists ? (int)(blockIdx.x & 7) : 0;
-    const int count = xcd_lists ? (E / 4) * 8 : E * ntl;
-    u32* ticket = a.epi.status + 16 + list;  // tickets live in the status block, after the word
-    auto tile_of = [&](int t, int& g, int& ct) {
-        if (xcd_lists) {
-            g = (list >> 1) + 4 * (t >> 3);
-            ct = (list & 1) * 8 + (t & 7);
-        } else {
-            g = t / ntl;
-            ct = t % ntl;
-        }
-    };
+    const int count = a.gt.n_groups * ntl;
+    u32* ticket = a.epi.status + 16;  // the ticket lives in the status block, after the word
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int q = lane >> 4, c = lane & 15;
     if (threadIdx.x == 0) next_t = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -245,8 +233,7 @@ __global__ __launch_bounds__(256, 2) void gmsq_decode_kernel(const GemmArgs a, c
         // draw the next ticket now; its result is needed only after this tile
         u32 nt_pending = 0;
         if (threadIdx.x == 0) nt_pending = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        int g, ct;
-        tile_of(t, g, ct);
+        const int g = t / ntl, ct = t % ntl;
         const int r0 = g ? a.gt.row_end[g - 1] : 0;
         const int r1 = a.gt.row_end[g];
         if (r0 < r1) {

@@ -312,7 +312,7 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
     }
     if (fast && a.gt.max_rows <= kSkinnyMaxRows && aligned(y, 16)) {
         // decode-shaped groups: weight streaming with the requant fused (per-expert exchange), on a
-        // persistent grid of two workgroups per CU drawing tiles from per-XCD lists
+        // persistent grid of two workgroups per CU drawing tiles from one ticket in expert order
         const int cus = device_cus();
         int resident = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, (const void*)gmsq_decode_kernel, 256, 0) !=
@@ -323,11 +323,10 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
         if (grid > tiles) grid = (int)tiles;
         if (grid >= 1) {
             a.ntiles = ntl;
-            const int xcd_lists = 0;  // measured: one list in expert order beats per-XCD lists
             clear_ws(tiles);
             {
                 TimedLaunch timed(st);
-                hipLaunchKernelGGL(gmsq_decode_kernel, dim3((unsigned)grid), dim3(256), 0, st, a, xcd_lists);
+                hipLaunchKernelGGL(gmsq_decode_kernel, dim3((unsigned)grid), dim3(256), 0, st, a);
             }
             hipLaunchKernelGGL(gmsq_decode_fixup_kernel, dim3((unsigned)(tiles < 512 ? tiles : 512)), dim3(256), 0, st, a);
             return check_launch();
