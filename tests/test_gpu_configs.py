@@ -1,10 +1,9 @@
 """GPU parity at the benchmark configurations' full sizes.
 
-Whole-tensor oracle comparisons where the CPU oracle finishes in seconds (DynamicQuant,
-AddRmsNormDynamicQuant, QuantMatmul), sampled experts / rows for the MoE configurations (the
-oracle is checked on whole experts, including every partial 256-row tile of them), and
-size-independent properties on every row: |y| <= 127, the row maximum lands on 126/127, scales are
-finite and positive, the int32 core is bit-exact.
+Whole-tensor oracle comparisons (DynamicQuant, AddRmsNormDynamicQuant, QuantMatmul, and every row
+of both GroupedMatmulSwigluQuant configurations, expert by expert; the C oracle takes tens of
+seconds on the prefill one), and size-independent properties on every row: |y| <= 127, the row
+maximum lands on 126/127, scales are finite and positive, the int32 core is bit-exact.
 """
 import importlib
 
@@ -84,6 +83,9 @@ def test_gmsq_prefill_int32_core_exact(cb, orc, prefill):
 
 
 def test_gmsq_prefill_config4(cb, orc, prefill):
+    """Every row of config 4 (131072 rows over 256 Zipf-routed experts) against the C oracle:
+    y_scale within 1e-5 relative, int8 within +-1 on at most 1% of elements, per expert, so that
+    every group end inside a persistent 256-row tile is compared."""
     d = prefill
     y, ys = cb.grouped_matmul_swiglu_quant(d["x"], d["weight"], d["weight_scale"], d["x_scale"], d["group_list"])
     torch.cuda.synchronize()
@@ -93,24 +95,13 @@ def test_gmsq_prefill_config4(cb, orc, prefill):
     rmax = np.abs(yn.astype(np.int32)).max(axis=1)
     assert np.isin(rmax, [126, 127]).all()
     assert np.isfinite(ysn).all() and (ysn > 0).all()
-    # whole sampled experts against the oracle (heavy, mid and the lightest expert)
-    experts, starts = _sample_experts(d["group_list"], 6, seed=2)
-    ws = d["weight_scale"].cpu().numpy()
-    xs = d["x_scale"].cpu().numpy()
-    def check(g, r0, r1):
-        yr, ysr = orc.gmsq(d["x"][r0:r1].cpu().numpy(), d["weight"][g:g + 1].cpu().numpy(), ws[g:g + 1],
-                           xs[r0:r1], np.array([r1 - r0]))
-        np.testing.assert_allclose(ysn[r0:r1], ysr, rtol=1e-5, err_msg=f"expert {g} rows {r0}:{r1}")
-        int8_close(yn[r0:r1], yr)
-
-    for g in experts:
-        s, e = starts[g], d["group_list"][g]
-        check(g, s, min(e, s + 700))
-        if e - s > 700:
-            # the expert's last 256-row tile (partial unless the rows divide by 256) and the full
-            # tile before it: the group end inside a persistent tile
-            last = s + ((e - s - 1) // 256) * 256
-            check(g, max(s + 700, last - 256), e)
+    gl = d["group_list"]
+    yr, ysr = orc.gmsq(d["x"].cpu().numpy(), d["weight"].cpu().numpy(), d["weight_scale"].cpu().numpy(),
+                       d["x_scale"].cpu().numpy(), np.array(gl))
+    for g, (s, e) in enumerate(zip([0] + gl[:-1], gl)):
+        if e > s:
+            np.testing.assert_allclose(ysn[s:e], ysr[s:e], rtol=1e-5, err_msg=f"expert {g} rows {s}:{e}")
+            int8_close(yn[s:e], yr[s:e])
 
 
 def test_gmsq_prefill_config4_gathered(cb, prefill):
@@ -170,7 +161,8 @@ def test_gmsq_decode_and_down_config5(cb, orc):
     torch.cuda.synchronize()
     yn, ysn, outn = y.cpu().numpy(), ys.cpu().numpy(), bits16(out)
     assert np.isin(np.abs(yn.astype(np.int32)).max(axis=1), [126, 127]).all()
-    experts, starts = _sample_experts(d["group_list"], 24, seed=3)
+    starts = [0] + d["group_list"][:-1]
+    experts = [g for g in range(len(starts)) if d["group_list"][g] > starts[g]]
     ws = d["weight_scale"].cpu().numpy()
     xs = d["x_scale"].cpu().numpy()
     ws2 = d["down_weight_scale"].cpu().numpy()
