@@ -121,6 +121,29 @@ def test_gmsq_prefill_config4_gathered(cb, prefill):
     del y1, y2, xg
 
 
+def test_down_projection_prefill_size(cb, orc, prefill):
+    """The int8 grouped down-projection at the bench's prefill size (x int8 [131072, 2048] over the
+    prefill Zipf routing, weights [256, 2048, 7168], bf16 out), every row bit-exact against the
+    oracle: the persistent dequant GEMM over full, partial and single-tile groups."""
+    gl = prefill["group_list"]
+    M = prefill["x"].shape[0]
+    r = cfgs.streams(41, 4)
+    x = cfgs.rand_i8((M, 2048), "cuda", r[0])
+    xs = cfgs.rand_uniform((M,), 0.005, 0.02, "cuda", r[1])
+    w = cfgs.rand_i8((256, 2048, 7168), "cuda", r[2])
+    ws = cfgs.rand_uniform((256, 7168), 0.001, 0.01, "cuda", r[3])
+    out = cb.grouped_matmul_quant(x, w, ws, xs, gl)
+    torch.cuda.synchronize()
+    outn = bits16(out)
+    del out
+    outr = orc.grouped_matmul_quant(x.cpu().numpy(), w.cpu().numpy(), ws.cpu().numpy(), xs.cpu().numpy(),
+                                    np.array(gl))
+    for g, (s, e) in enumerate(zip([0] + gl[:-1], gl)):
+        if e > s:
+            np.testing.assert_array_equal(outn[s:e], outr[s:e], err_msg=f"expert {g} rows {s}:{e}")
+    del x, w
+
+
 def test_gmsq_prefill_every_row_vs_int32_core(cb, prefill):
     """Every row of the prefill config: the operator (persistent GEMM with the cross-tile row-max
     exchange) against the exact int32 core plus a plain torch fp32 epilogue on the device (the
