@@ -278,7 +278,10 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
     const bool fast = K > 0 && K % 16 == 0 && H % 16 == 0 && offsets32_ok(K, N) && aligned(x, 16) &&
                       aligned(weight, 16) && aligned(weight_scale, 4);
     const int ntl = (int)((H + 127) / 128);  // 128-act-column tiles
-    if (fast && a.gt.max_rows > kSkinnyMaxRows && aligned(y, 4)) {
+    // a test that turns the persistent launches off also takes the two-pass path here: the path
+    // taken when the fused kernels' grids cannot all be resident
+    const bool fused = g_overrides.persistent_grid >= 0;
+    if (fused && fast && a.gt.max_rows > kSkinnyMaxRows && aligned(y, 4)) {
         // prefill-shaped groups: the persistent GEMM with the requant fused
         const int cus = device_cus();
         const int grid = (ntl == 16 && cus >= 256) ? 256 : (cus / ntl) * ntl;
@@ -310,7 +313,7 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
             return check_launch();
         }
     }
-    if (fast && a.gt.max_rows <= kSkinnyMaxRows && aligned(y, 16)) {
+    if (fused && fast && a.gt.max_rows <= kSkinnyMaxRows && aligned(y, 16)) {
         // decode-shaped groups: weight streaming with the requant fused (per-expert exchange), on a
         // persistent grid of two workgroups per CU drawing tiles from one ticket in expert order
         const int cus = device_cus();

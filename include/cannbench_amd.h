@@ -190,7 +190,8 @@ int cb_grouped_matmul_swiglu_quant_noalloc(const int8_t* x, const int8_t* weight
  * thread's later launches, kept until changed; 0 restores each default:
  *   persistent_grid      workgroups of the persistent dequant / int32 GEMM (default: the CU count;
  *                        a small grid makes every workgroup walk many tiles); < 0 turns that
- *                        persistent launch off.
+ *                        persistent launch off, and GroupedMatmulSwigluQuant then takes its
+ *                        two-pass path (the one it takes when its fused grid cannot be resident).
  *   exchange_spin_limit  polls of the GroupedMatmulSwigluQuant row-maximum exchange before a tile
  *                        gives up and leaves its output to the fix-up launch (default 2^20, about
  *                        2 s); a small value exercises the fix-up path, a negative one makes every
