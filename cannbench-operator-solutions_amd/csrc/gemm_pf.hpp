@@ -15,7 +15,8 @@
 // of apply_deq per element (the common chain - per-channel scale, optional per-token scale, bf16
 // out - without the selects), a 4 x 4 transpose of 16-bit values across each lane quad so that a
 // lane holds 4 consecutive columns of one row, and 8-byte stores through a resource over the
-// tile's valid rows (columns past N go outside it).
+// tile's valid rows (columns past N go outside it); with N a multiple of 8, a swap between lanes
+// c and c ^ 4 gives each lane 8 columns of one row and the stores are 16 bytes.
 #pragma once
 
 #include "gmsq_prefill.hpp"
@@ -262,7 +263,8 @@ __device__ __forceinline__ void gpf_epilogue(const GemmArgs& a, uint8_t* smem, v
 }
 
 // Persistent launch: gridDim.x workgroups (at most one per CU) walk the launch order's slots.
-// Batch 1, K of at least 4 stages, N a multiple of 4 (8-byte stores), bf16 / fp16 out.
+// Batch 1, K of at least 4 stages, N a multiple of 4 (8-byte stores; 16-byte with N a multiple of 8),
+// bf16 / fp16 out.
 template <bool SIMPLE>
 __global__ __launch_bounds__(256, 1) void gpf_dequant_kernel(const GemmArgs a)
 {

@@ -153,7 +153,7 @@ static void launch_gemm(GemmArgs& a, const int64_t* gl, int64_t E, int64_t batch
     const int pg = persistent_grid();
     if constexpr (EPI == EPI_DEQUANT) {
         // the four-wave ring core with a continuous stage stream (K of at least 4 stages) and
-        // 8-byte stores of 4 columns (N a multiple of 4)
+        // 8-byte stores of 4 columns (N a multiple of 4; 16 bytes of 8 columns with N a multiple of 8)
         if (batch == 1 && pg > 0 && a.K >= 4 * PfCfg::BK && Ncols % 4 == 0 && 256 * Ncols * 2 < 0x7fffffffLL) {
             const EpiArgs& e = a.epi;
             const bool simple = !e.has_offset && e.bias_kind == BIAS_NONE && e.out_bf16;
