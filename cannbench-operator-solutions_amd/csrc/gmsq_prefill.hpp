@@ -918,6 +918,46 @@ struct PfDefer {
         // lane (h, c) holds rows (2 fm + wm) * 32 + 8 q + 4 h + i of column c: rint16 of
         // act * (127 / amax), a 4 x 4 byte transpose across each lane quad (lane qi ends with row
         // + qi, columns (c & ~3) .. +3), one dword store per 32-column half
+        auto quad_bytes = [&](const int fm, const int q, const int j, const v4f& inv4) -> u32 {
+            // clamp-and-narrow == saturating rint16; an all-zero row gives 0 * inf = NaN -> 0
+            const u32 x = pack4_i8(rint16_h(act[fm][j][4 * q + 0] * inv4[0]), rint16_h(act[fm][j][4 * q + 1] * inv4[1]),
+                                   rint16_h(act[fm][j][4 * q + 2] * inv4[2]), rint16_h(act[fm][j][4 * q + 3] * inv4[3]));
+            // step 1 swaps 16-bit halves with lane qi ^ 2, step 2 bytes with qi ^ 1
+            const u32 pp = (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false);
+            const u32 z = (qi & 2) ? __builtin_amdgcn_perm(x, pp, 0x07060302u) : __builtin_amdgcn_perm(pp, x, 0x05040100u);
+            const u32 pz = (u32)__builtin_amdgcn_update_dpp(0, (int)z, 0xB1, 0xF, 0xF, false);
+            return (qi & 1) ? __builtin_amdgcn_perm(pz, z, 0x03070105u) : __builtin_amdgcn_perm(pz, z, 0x06020400u);
+        };
+        if ((H & 7) == 0 && ((uintptr_t)e.yq & 7) == 0) {
+            // 8-byte stores: slices q and q + 1 transposed, then one swap with lane c ^ 4 (ds_swizzle,
+            // lane-uniform): the lane with bit 2 of c clear keeps slice q's row with columns 4..7
+            // from lane c + 4, the other slice q + 1's row with columns 0..3 from lane c - 4
+            const bool hi4 = (c >> 2) & 1;
+            uint32_t ybase8[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int cl = wn * 64 + j * 32 + (c & ~7);
+                ybase8[j] = c0 + cl < H ? (uint32_t)((wm * 32 + 4 * h + qi) * H + cl) : 0x80000000u;
+            }
+#pragma unroll
+            for (int fm = 0; fm < 4; ++fm) {
+#pragma unroll
+                for (int qp = 0; qp < 2; ++qp) {
+                    const v4f ia = *(const CB_LDS v4f*)(inv_l + (2 * fm + wm) * 32 + 16 * qp + 4 * h);
+                    const v4f ib = *(const CB_LDS v4f*)(inv_l + (2 * fm + wm) * 32 + 16 * qp + 8 + 4 * h);
+                    const uint32_t roff = (uint32_t)((64 * fm + 16 * qp + (hi4 ? 8 : 0)) * H);
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const u32 ya = quad_bytes(fm, 2 * qp, j, ia), yb = quad_bytes(fm, 2 * qp + 1, j, ib);
+                        const u32 r = (u32)__builtin_amdgcn_ds_swizzle((int)(hi4 ? ya : yb), 0x101F);
+                        typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+                        const v2u w = hi4 ? v2u{r, yb} : v2u{ya, r};
+                        __builtin_amdgcn_raw_buffer_store_b64(w, yr, ybase8[j] + roff, 0, 0);
+                    }
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int fm = 0; fm < 4; ++fm) {
 #pragma unroll
@@ -925,17 +965,8 @@ struct PfDefer {
                 const v4f inv4 = *(const CB_LDS v4f*)(inv_l + (2 * fm + wm) * 32 + 8 * q + 4 * h);
                 const uint32_t roff = (uint32_t)((64 * fm + 8 * q) * H);  // rows below slice (0, 0)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    // clamp-and-narrow == saturating rint16; an all-zero row gives 0 * inf = NaN -> 0
-                    const u32 x = pack4_i8(rint16_h(act[fm][j][4 * q + 0] * inv4[0]), rint16_h(act[fm][j][4 * q + 1] * inv4[1]),
-                                           rint16_h(act[fm][j][4 * q + 2] * inv4[2]), rint16_h(act[fm][j][4 * q + 3] * inv4[3]));
-                    // step 1 swaps 16-bit halves with lane qi ^ 2, step 2 bytes with qi ^ 1
-                    const u32 pp = (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false);
-                    const u32 z = (qi & 2) ? __builtin_amdgcn_perm(x, pp, 0x07060302u) : __builtin_amdgcn_perm(pp, x, 0x05040100u);
-                    const u32 pz = (u32)__builtin_amdgcn_update_dpp(0, (int)z, 0xB1, 0xF, 0xF, false);
-                    const u32 y = (qi & 1) ? __builtin_amdgcn_perm(pz, z, 0x03070105u) : __builtin_amdgcn_perm(pz, z, 0x06020400u);
-                    __builtin_amdgcn_raw_buffer_store_b32((int)y, yr, ybase[j] + roff, 0, 0);
-                }
+                for (int j = 0; j < 2; ++j)
+                    __builtin_amdgcn_raw_buffer_store_b32((int)quad_bytes(fm, q, j, inv4), yr, ybase[j] + roff, 0, 0);
             }
         }
     }
