@@ -1,12 +1,14 @@
 """Benchmark of the W8A8 MoE-FFN hot path on one MI355X.
 
 Headline (`value`): GroupedMatmulSwigluQuant on the prefill configuration (131072 int8 rows,
-256 experts, K 7168, N 4096, Zipf(1.1) routing), in TOPS = 2*M*K*N / wall time of the whole op
+256 experts, K 7168, N 4096, Zipf(1.1) routing), in TOPS = 2*M*K*N / device time of the whole op
 (all of its kernels), inputs resident in HBM.  The same JSON line also carries the decode
 configuration (GB/s of algorithmic bytes), its down-projection, AddRmsNormDynamicQuant, the
 dense QuantMatmul and the routing operators (gating, re-routing, finalize, DequantSwigluQuant),
-each with its own roofline figure, plus a CPU baseline (the C oracle on a
-bounded sample of the prefill rows, on the host cores).
+each with its own roofline figure, plus CPU baselines (the C oracle on bounded samples of the
+prefill and decode experts, on the host cores).  Every time is the median over the timed calls of
+HIP events around each call; configs 2 and 3 (whose inputs would fit the 256 MB MALL) are preceded
+by a 512 MB flush write outside the events.
 
 A step is one operator call over one batch of synthetic input.  Usage:
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only prefill,decode,...] [--no-cpu]
@@ -50,22 +52,49 @@ class KernelTimer:
         self.i += 1
         L.load().cb_set_kernel_timing(a.cuda_event, b.cuda_event)
 
-    def mean_ms(self):
+    def median_ms(self):
         ts = [a.elapsed_time(b) for a, b in self.pairs[: self.i]]
-        return float(np.mean(ts)) if ts else None
+        return float(np.median(ts)) if ts else None
 
 
-def time_op(fn, steps, warmup, timer=None):
+FLUSH_BYTES = 512 << 20  # twice the 256 MB MALL: a write of it evicts every cache level
+
+
+class Flush:
+    """A 512 MB device write issued before a timed call, outside its events, so that the call's
+    inputs come from HBM rather than the 256 MB MALL or the L2s (SURVEY 8(d) for configs 2 and 3)."""
+
+    def __init__(self, dev):
+        self.buf = torch.empty(FLUSH_BYTES // 4, dtype=torch.int32, device=dev)
+        self.k = 0
+
+    def __call__(self):
+        self.k += 1
+        self.buf.fill_(self.k)
+
+
+def time_op(fn, steps, warmup, timer=None, flush=None):
+    """Per-call device time of `fn` (HIP events on the current stream, which the operators enqueue
+    on), median over `steps` calls after `warmup` untimed ones.  `flush`, when given, runs before
+    every call, outside the events.  Returns (median ms, mean wall ms per call of the timed loop)."""
     for _ in range(warmup):
+        if flush is not None:
+            flush()
         fn()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(steps):
+    for a, b in ev:
+        if flush is not None:
+            flush()
         if timer is not None:
             timer.arm()
+        a.record()
         fn()
+        b.record()
     torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e3 / steps
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return float(np.median([a.elapsed_time(b) for a, b in ev])), wall
 
 
 def roofline(bound, achieved, unit, traffic=None, peak=None):
@@ -83,10 +112,10 @@ def bench_prefill(steps, warmup, dev, keep):
     ops = 2.0 * M * K * N
     fn = lambda: cb.grouped_matmul_swiglu_quant(d["x"], d["weight"], d["weight_scale"], d["x_scale"], d["group_list"])
     timer = KernelTimer(steps)
-    ms = time_op(fn, steps, warmup, timer)
-    kms = timer.mean_ms()
+    ms, wall = time_op(fn, steps, warmup, timer)
+    kms = timer.median_ms()
     counts = np.diff([0] + d["group_list"])
-    res = {"ms": ms, "tops": ops / (ms * 1e-3) / 1e12, "gemm_kernel_ms": kms,
+    res = {"ms": ms, "wall_ms": wall, "tops": ops / (ms * 1e-3) / 1e12, "gemm_kernel_ms": kms,
            "roofline": roofline("mfma", ops / (kms * 1e-3) / 1e12, "TFLOP/s"),
            "config": {"workload": "gmsq_prefill", "rows": M, "experts": len(counts), "K": K, "N": N,
                       "routing": "zipf(1.1) multinomial, numpy seed 0",
@@ -114,12 +143,12 @@ def bench_prefill_gather(steps, warmup, dev, keep):
     fused = lambda: cb.grouped_matmul_swiglu_quant_gather(x_tok, idx, d["weight"], d["weight_scale"], xs_tok,
                                                           d["group_list"])
     timer = KernelTimer(steps)
-    ms = time_op(fused, steps, warmup, timer)
-    kms = timer.mean_ms()
+    ms, _ = time_op(fused, steps, warmup, timer)
+    kms = timer.median_ms()
     il = idx.long()
     unfused = lambda: cb.grouped_matmul_swiglu_quant(x_tok.index_select(0, il), d["weight"], d["weight_scale"],
                                                      xs_tok.index_select(0, il), d["group_list"])
-    ms_u = time_op(unfused, steps, warmup)
+    ms_u, _ = time_op(unfused, steps, warmup)
     return {"value": round(ops / (ms * 1e-3) / 1e12, 2), "unit": "TOPS", "ms_per_step": round(ms, 4),
             "gemm_kernel_ms": round(kms, 4), "roofline": roofline("mfma", ops / (kms * 1e-3) / 1e12, "TFLOP/s"),
             "unfused_ms_per_step": round(ms_u, 4), "saving_ms": round(ms_u - ms, 4),
@@ -141,8 +170,8 @@ def bench_down_prefill(steps, warmup, dev, keep):
     ops = 2.0 * M * 2048 * 7168
     fn = lambda: cb.grouped_matmul_quant(x, w, ws, xs, d["group_list"])
     timer = KernelTimer(steps)
-    ms = time_op(fn, steps, warmup, timer)
-    kms = timer.mean_ms()
+    ms, _ = time_op(fn, steps, warmup, timer)
+    kms = timer.median_ms()
     del x, w
     return {"value": round(ops / (ms * 1e-3) / 1e12, 2), "unit": "TOPS", "ms_per_step": round(ms, 4),
             "gemm_kernel_ms": round(kms, 4), "roofline": roofline("mfma", ops / (kms * 1e-3) / 1e12, "TFLOP/s"),
@@ -158,14 +187,15 @@ def decode_bytes(counts, K, N):
 
 def bench_decode(steps, warmup, dev, keep):
     d = cfgs.make_gmsq_decode(dev)
+    keep["decode"] = d
     M, K = d["x"].shape
     E, _, N = d["weight"].shape
     counts = np.diff([0] + d["group_list"])
     nbytes = decode_bytes(counts, K, N)
     fn = lambda: cb.grouped_matmul_swiglu_quant(d["x"], d["weight"], d["weight_scale"], d["x_scale"], d["group_list"])
     timer = KernelTimer(steps)
-    ms = time_op(fn, steps, warmup, timer)
-    kms = timer.mean_ms()
+    ms, _ = time_op(fn, steps, warmup, timer)
+    kms = timer.median_ms()
     res = {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes, "gemm_kernel_ms": kms,
            "roofline": roofline("hbm", nbytes / (kms * 1e-3) / 1e9, "GB/s"),
            "config": {"workload": "gmsq_decode", "rows": M, "experts": E, "K": K, "N": N,
@@ -179,8 +209,8 @@ def bench_decode(steps, warmup, dev, keep):
     b2 = act_e * K2 * N2 + M * K2 + 2 * M * N2 + 4 * M + 4 * N2 * act_e
     fn2 = lambda: cb.grouped_matmul_quant(y, w2, ws2, ys, d["group_list"])
     timer2 = KernelTimer(steps)
-    ms2 = time_op(fn2, steps, warmup, timer2)
-    k2 = timer2.mean_ms()
+    ms2, _ = time_op(fn2, steps, warmup, timer2)
+    k2 = timer2.median_ms()
     down = {"ms": ms2, "gbs": b2 / (ms2 * 1e-3) / 1e9, "bytes": b2, "gemm_kernel_ms": k2,
             "roofline": roofline("hbm", b2 / (k2 * 1e-3) / 1e9, "GB/s"),
             "config": {"workload": "down_proj", "rows": M, "K": K2, "N": N2, "experts": E}}
@@ -193,8 +223,8 @@ def bench_ardq(steps, warmup, dev):
     nbytes = 2 * (2 * R * H) + 2 * H + 2 * R * H + R * H + 4 * R
     fn = lambda: cb.add_rms_norm_dynamic_quant(d["x1"], d["x2"], d["gamma"], d["epsilon"])
     timer = KernelTimer(steps)
-    ms = time_op(fn, steps, warmup, timer)
-    kms = timer.mean_ms()
+    ms, _ = time_op(fn, steps, warmup, timer, flush=Flush(dev))
+    kms = timer.median_ms()
     return {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes, "kernel_ms": kms,
             "roofline": roofline("hbm", nbytes / (kms * 1e-3) / 1e9, "GB/s"),
             "config": {"workload": "ardq", "rows": R, "cols": H, "dtype": "bf16"}}
@@ -208,8 +238,8 @@ def bench_qmm(steps, warmup, dev):
     fn = lambda: cb.quant_matmul(d["x1"], d["x2"], d["scale"], pertoken_scale=d["pertoken_scale"],
                                  output_dtype="bfloat16")
     timer = KernelTimer(steps)
-    ms = time_op(fn, steps, warmup, timer)
-    kms = timer.mean_ms()
+    ms, _ = time_op(fn, steps, warmup, timer, flush=Flush(dev))
+    kms = timer.median_ms()
     return {"ms": ms, "tops": ops / (ms * 1e-3) / 1e12, "gemm_kernel_ms": kms,
             "roofline": roofline("mfma", ops / (kms * 1e-3) / 1e12, "TFLOP/s"),
             "config": {"workload": "qmm", "M": M, "K": K, "N": N}}
@@ -228,15 +258,15 @@ def bench_gmm(steps, warmup, dev):
     flops = 2.0 * E * rows * K * N
     fn = lambda: cb.grouped_matmul(x, w, gl, bias=b, split_item=2)
     timer = KernelTimer(steps)
-    ms = time_op(fn, steps, warmup, timer)
-    kms = timer.mean_ms()
+    ms, _ = time_op(fn, steps, warmup, timer)
+    kms = timer.median_ms()
     # the same problem with the weight stored [E, N, K] (transpose_weight), and the vendor batched
     # bf16 GEMM (torch.bmm -> hipBLASLt, no bias) on the equal-sized groups, wall-clock timed
     wt = w.transpose(1, 2).contiguous()
-    ms_t = time_op(lambda: cb.grouped_matmul(x, wt, gl, bias=b, split_item=2, transpose_weight=True), steps, warmup)
+    ms_t, _ = time_op(lambda: cb.grouped_matmul(x, wt, gl, bias=b, split_item=2, transpose_weight=True), steps, warmup)
     del wt
     xb = x.view(E, rows, K)
-    ms_v = time_op(lambda: torch.bmm(xb, w), steps, warmup)
+    ms_v, _ = time_op(lambda: torch.bmm(xb, w), steps, warmup)
     return {"value": round(flops / (ms * 1e-3) / 1e12, 1), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
             "kernel_ms": round(kms, 4),
             "transpose_weight_tflops": round(flops / (ms_t * 1e-3) / 1e12, 1),
@@ -258,7 +288,7 @@ def bench_vendor(steps, warmup, dev):
     res = {"op": "torch._int_mm (hipBLASLt)", "M": M, "K": K, "N": N}
     for name, w in (("n_contiguous", x2), ("k_contiguous", x2.t().contiguous().t())):
         try:
-            ms = time_op(lambda: torch._int_mm(x1, w), steps, warmup)
+            ms, _ = time_op(lambda: torch._int_mm(x1, w), steps, warmup)
             res[name] = {"tops": round(ops / (ms * 1e-3) / 1e12, 1), "ms": round(ms, 4)}
         except Exception as exc:  # reported, not fatal: the vendor path is context only
             res[name] = {"error": str(exc).splitlines()[0][:200]}
@@ -297,8 +327,8 @@ def _hbm_entry(fn, nbytes, steps, warmup, config):
     """value: algorithmic bytes / wall time of the whole op call (host wrapper included);
     roofline: the same bytes / device time of the op's kernels (HIP events on its stream)."""
     timer = KernelTimer(steps)
-    ms = time_op(fn, steps, warmup, timer)
-    kms = timer.mean_ms()
+    ms, _ = time_op(fn, steps, warmup, timer)
+    kms = timer.median_ms()
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(ms, 4), "kernel_ms": round(kms, 4),
             "bytes": int(nbytes), "roofline": roofline("hbm", nbytes / (kms * 1e-3) / 1e9, "GB/s"), "config": config}
@@ -344,7 +374,7 @@ def bench_copy(steps, warmup, dev):
     n = 2 << 30
     a = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
     b = torch.empty_like(a)
-    ms = time_op(lambda: b.copy_(a), steps, warmup)
+    ms, _ = time_op(lambda: b.copy_(a), steps, warmup)
     return {"ms": ms, "gbs": 2 * n / (ms * 1e-3) / 1e9, "bytes_read": n, "bytes_written": n}
 
 
@@ -404,6 +434,40 @@ def cpu_baseline(d, budget_s=12.0):
                       f"of the prefill config, {t_total:.1f} s"}
 
 
+def cpu_baseline_decode(d, budget_s=8.0):
+    """The C oracle on the host cores over whole experts of the decode config (config 5), until
+    ~budget_s, in GB/s of the same algorithmic bytes as the GPU figure: each active expert's weights
+    once, its rows of x, y and the scales."""
+    from oracle import oracle as orc
+    gl = d["group_list"]
+    starts = [0] + gl[:-1]
+    K = d["x"].shape[1]
+    N = d["weight"].shape[2]
+    ws = d["weight_scale"].cpu().numpy()
+    xs = d["x_scale"].cpu().numpy()
+    nbytes, t_total, experts, rows = 0, 0.0, 0, 0
+    for g in range(len(gl)):
+        s, e = starts[g], gl[g]
+        if e == s:
+            continue
+        x = d["x"][s:e].cpu().numpy()
+        w = d["weight"][g:g + 1].cpu().numpy()
+        t0 = time.perf_counter()
+        orc.gmsq(x, w, ws[g:g + 1], xs[s:e], np.array([e - s]))
+        t_total += time.perf_counter() - t0
+        nbytes += decode_bytes([e - s], K, N)
+        experts += 1
+        rows += e - s
+        if t_total >= budget_s:
+            break
+    cores = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        cores = min(cores, int(os.environ["OMP_NUM_THREADS"]))
+    return {"value": round(nbytes / t_total / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"oracle/cb_oracle.c or_gmsq (OpenMP) on {experts} whole experts ({rows} rows) of the "
+                      f"decode config, {t_total:.1f} s"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -435,6 +499,10 @@ def main():
         p = bench_prefill(args.steps, args.warmup, dev, keep)
         out.update(value=round(p["tops"], 2), ms_per_step=round(p["ms"], 4), config=p["config"],
                    roofline=p["roofline"])
+        out["timing"] = ("ms_per_step: median over the timed calls of HIP events around each whole "
+                         "operator call (every kernel it launches); wall_ms_per_step: host clock over "
+                         "the timed loop / steps")
+        out["wall_ms_per_step"] = round(p["wall_ms"], 4)
         out["prefill_gemm_kernel_ms"] = round(p["gemm_kernel_ms"], 4)
         out["frac_of_int8_peak"] = round(p["tops"] / PEAK_INT8_TOPS, 4)
         if "gather" in only:
@@ -479,6 +547,8 @@ def main():
             out["routing"][name]["roofline"]["traffic"] = traffic_from_profiles("routing_" + name, ROUTING_KERNELS[name])
     if not args.no_cpu and "prefill" in keep:
         out["cpu_baseline"] = cpu_baseline(keep["prefill"])
+    if not args.no_cpu and "decode" in keep:
+        out["decode"]["cpu_baseline"] = cpu_baseline_decode(keep["decode"])
     print(json.dumps(out), flush=True)
 
 

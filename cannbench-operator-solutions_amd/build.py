@@ -61,5 +61,30 @@ def build(verbose=False, defines=(), out=LIB_PATH, obj_dir=OBJ_DIR):
     return out
 
 
+# Host-side AddressSanitizer + UBSan build of the same sources (the device code is unchanged: the
+# sanitizers apply to the host passes only).  Test infrastructure: tests/test_sanitize.py loads it
+# into a process that preloads the clang ASan runtime and runs the CPU tests (every validation
+# branch of the C ABI, no GPU) against it.
+SAN_DIR = os.path.join(OBJ_DIR, "san")
+SAN_LIB = os.path.join(SAN_DIR, "libcannbench_amd_san.so")
+SAN_FLAGS = ["-g", "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+             "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer"]
+
+
+def build_sanitized():
+    """The sanitized library (rebuilt only when a source or header is newer than it)."""
+    deps = [os.path.join(CSRC, f) for f in os.listdir(CSRC)] + [
+        os.path.join(os.path.dirname(PKG_DIR), "include", "cannbench_amd.h"), os.path.abspath(__file__)]
+    if os.path.exists(SAN_LIB) and os.path.getmtime(SAN_LIB) >= max(os.path.getmtime(d) for d in deps):
+        return SAN_LIB
+    global HIP_FLAGS
+    saved = HIP_FLAGS
+    HIP_FLAGS = saved + SAN_FLAGS
+    try:
+        return build(out=SAN_LIB, obj_dir=SAN_DIR)
+    finally:
+        HIP_FLAGS = saved
+
+
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))

@@ -327,7 +327,6 @@ __global__ __launch_bounds__(256, 2) void skinny_kernel(const GemmArgs a)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int q = lane >> 4, c = lane & 15;
     const int64_t K = a.K, N = a.N;
-    const EpiArgs& e = a.epi;
 
     const int64_t ocol = (int64_t)ct * 256 + 16 * c;  // first weight / output column of this lane
     const bool colok = ocol < N;

@@ -14,9 +14,9 @@
 // Epilogue, register direct (the ring already receives the next tile's stages): the dequant chain
 // of apply_deq per element (the common chain - per-channel scale, optional per-token scale, bf16
 // out - without the selects), a 4 x 4 transpose of 16-bit values across each lane quad so that a
-// lane holds 4 consecutive columns of one row, and 8-byte stores through a resource over the
-// tile's valid rows (columns past N go outside it); with N a multiple of 8, a swap between lanes
-// c and c ^ 4 gives each lane 8 columns of one row and the stores are 16 bytes.
+// lane holds 4 consecutive columns of one row, and stores through a resource over the
+// tile's valid rows (columns past N go outside it), after a swap between lanes c and c ^ 4 that
+// gives each lane 8 columns of one row, so the stores are 16 bytes.
 #pragma once
 
 #include "gmsq_prefill.hpp"
@@ -161,15 +161,12 @@ __device__ __forceinline__ void gpf_epilogue(const GemmArgs& a, uint8_t* smem, v
     const int vr = t.vrows < 256 ? t.vrows : 256;
     const __amdgpu_buffer_rsrc_t ores = make_rsrc((uint16_t*)e.out + (int64_t)t.m0 * N, (uint32_t)((int64_t)vr * N * 2));
     ColDeq cd[4];
-    uint32_t coff[4];
 #pragma unroll
     for (int fn = 0; fn < 4; ++fn) {
         const int tc = (fn >> 1) * 128 + wn * 64 + (fn & 1) * 32;
-        const int64_t cc = (int64_t)t.nt * 256 + tc + c;       // this lane's column (values)
-        const int64_t cq = (int64_t)t.nt * 256 + tc + (c & ~3);  // the quad's first column (stores)
+        const int64_t cc = (int64_t)t.nt * 256 + tc + c;  // this lane's column (values)
         if constexpr (SIMPLE) cd[fn] = ColDeq{cs_l[tc + c], 0.0f, 0.0f};
         else cd[fn] = col_deq(e, t.g, 0, cc < N ? cc : 0);
-        coff[fn] = cq < N ? (uint32_t)cq * 2u : 0x80000000u;
     }
     // the dequant chain of lane value i of accumulator slice (fm, fn, q) -> bf16 / fp16 pairs
     auto packed = [&](const int fm, const int fn, const int q, const v4f& xs4, u32& p01, u32& p23) {
@@ -188,83 +185,50 @@ __device__ __forceinline__ void gpf_epilogue(const GemmArgs& a, uint8_t* smem, v
             p23 = (u32)f32_to_f16(f[2]) | ((u32)f32_to_f16(f[3]) << 16);
         }
     };
-    if ((N & 7) == 0) {
-        // 16-byte stores: after the quad transposes of slices q and q + 1, lanes c and c ^ 4 hold
-        // columns 0..3 and 4..7 of the same 8-column group for rows of both slices; the lane with
-        // bit 2 of c clear keeps slice q's row and takes columns 4..7 from lane c + 4, the other
-        // keeps slice q + 1's row and takes columns 0..3 from lane c - 4, so each lane stores 8
-        // contiguous columns of one row
-        const bool hi4 = (c >> 2) & 1;
-        uint32_t coff8[4];
+    // 16-byte stores (the launch requires N % 8 == 0 and a 16-byte aligned output).
+    // 16-byte stores: after the quad transposes of slices q and q + 1, lanes c and c ^ 4 hold
+    // columns 0..3 and 4..7 of the same 8-column group for rows of both slices; the lane with
+    // bit 2 of c clear keeps slice q's row and takes columns 4..7 from lane c + 4, the other
+    // keeps slice q + 1's row and takes columns 0..3 from lane c - 4, so each lane stores 8
+    // contiguous columns of one row
+    const bool hi4 = (c >> 2) & 1;
+    uint32_t coff8[4];
 #pragma unroll
-        for (int fn = 0; fn < 4; ++fn) {
-            const int64_t c8 = (int64_t)t.nt * 256 + (fn >> 1) * 128 + wn * 64 + (fn & 1) * 32 + (c & ~7);
-            coff8[fn] = c8 < N ? (uint32_t)c8 * 2u : 0x80000000u;
-        }
-#pragma unroll
-        for (int fm = 0; fm < 4; ++fm) {
-#pragma unroll
-            for (int qp = 0; qp < 2; ++qp) {
-                const int row0 = (2 * fm + wm) * 32 + 16 * qp + 4 * h;  // slice 2 qp; slice 2 qp + 1 is 8 rows on
-                const v4f xa = *(const CB_LDS v4f*)(xs_l + row0);
-                const v4f xb = *(const CB_LDS v4f*)(xs_l + row0 + 8);
-                const uint32_t roff = (uint32_t)(row0 + (hi4 ? 8 : 0) + qi) * (uint32_t)N * 2u;
-#pragma unroll
-                for (int fn = 0; fn < 4; ++fn) {
-                    u32 pa01, pa23, pb01, pb23, x0, x1, z0, z1;
-                    packed(fm, fn, 2 * qp, xa, pa01, pa23);
-                    packed(fm, fn, 2 * qp + 1, xb, pb01, pb23);
-                    quad_transpose16(pa01, pa23, qs, x0, x1);
-                    quad_transpose16(pb01, pb23, qs, z0, z1);
-                    // one lane-uniform exchange with lane c ^ 4 (ds_swizzle bit mode, xor mask 4): a
-                    // cross-lane read under a lane-dependent branch would see inactive lanes
-                    const u32 s0 = hi4 ? x0 : z0, s1 = hi4 ? x1 : z1;
-                    const u32 r0 = (u32)__builtin_amdgcn_ds_swizzle((int)s0, 0x101F);
-                    const u32 r1 = (u32)__builtin_amdgcn_ds_swizzle((int)s1, 0x101F);
-                    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-                    const v4u w = hi4 ? v4u{r0, r1, z0, z1} : v4u{x0, x1, r0, r1};
-                    __builtin_amdgcn_raw_buffer_store_b128(w, ores, roff + coff8[fn], 0, 0);
-                }
-            }
-        }
-        return;
+    for (int fn = 0; fn < 4; ++fn) {
+        const int64_t c8 = (int64_t)t.nt * 256 + (fn >> 1) * 128 + wn * 64 + (fn & 1) * 32 + (c & ~7);
+        coff8[fn] = c8 < N ? (uint32_t)c8 * 2u : 0x80000000u;
     }
 #pragma unroll
     for (int fm = 0; fm < 4; ++fm) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int row = (2 * fm + wm) * 32 + 8 * q + 4 * h;  // rows row .. row + 3
-            const v4f xs4 = *(const CB_LDS v4f*)(xs_l + row);
-            const uint32_t roff = (uint32_t)(row + qi) * (uint32_t)N * 2u;
+        for (int qp = 0; qp < 2; ++qp) {
+            const int row0 = (2 * fm + wm) * 32 + 16 * qp + 4 * h;  // slice 2 qp; slice 2 qp + 1 is 8 rows on
+            const v4f xa = *(const CB_LDS v4f*)(xs_l + row0);
+            const v4f xb = *(const CB_LDS v4f*)(xs_l + row0 + 8);
+            const uint32_t roff = (uint32_t)(row0 + (hi4 ? 8 : 0) + qi) * (uint32_t)N * 2u;
 #pragma unroll
             for (int fn = 0; fn < 4; ++fn) {
-                float f[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int acc_v = acc_read(acc[fm][fn][4 * q + i]);
-                    if constexpr (SIMPLE) f[i] = ((float)acc_v * cd[fn].scale) * xs4[i];
-                    else f[i] = apply_deq(e, cd[fn], acc_v, xs4[i]);
-                }
-                u32 p01, p23;
-                if (SIMPLE || e.out_bf16) {
-                    p01 = pack_bf16x2(f[0], f[1]);
-                    p23 = pack_bf16x2(f[2], f[3]);
-                } else {
-                    p01 = (u32)f32_to_f16(f[0]) | ((u32)f32_to_f16(f[1]) << 16);
-                    p23 = (u32)f32_to_f16(f[2]) | ((u32)f32_to_f16(f[3]) << 16);
-                }
-                u32 d0, d1;
-                quad_transpose16(p01, p23, qs, d0, d1);
-                typedef unsigned int v2u __attribute__((ext_vector_type(2)));
-                __builtin_amdgcn_raw_buffer_store_b64(v2u{d0, d1}, ores, roff + coff[fn], 0, 0);
+                u32 pa01, pa23, pb01, pb23, x0, x1, z0, z1;
+                packed(fm, fn, 2 * qp, xa, pa01, pa23);
+                packed(fm, fn, 2 * qp + 1, xb, pb01, pb23);
+                quad_transpose16(pa01, pa23, qs, x0, x1);
+                quad_transpose16(pb01, pb23, qs, z0, z1);
+                // one lane-uniform exchange with lane c ^ 4 (ds_swizzle bit mode, xor mask 4): a
+                // cross-lane read under a lane-dependent branch would see inactive lanes
+                const u32 s0 = hi4 ? x0 : z0, s1 = hi4 ? x1 : z1;
+                const u32 r0 = (u32)__builtin_amdgcn_ds_swizzle((int)s0, 0x101F);
+                const u32 r1 = (u32)__builtin_amdgcn_ds_swizzle((int)s1, 0x101F);
+                typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+                const v4u w = hi4 ? v4u{r0, r1, z0, z1} : v4u{x0, x1, r0, r1};
+                __builtin_amdgcn_raw_buffer_store_b128(w, ores, roff + coff8[fn], 0, 0);
             }
         }
     }
 }
 
 // Persistent launch: gridDim.x workgroups (at most one per CU) walk the launch order's slots.
-// Batch 1, K of at least 4 stages, N a multiple of 4 (8-byte stores; 16-byte with N a multiple of 8),
-// bf16 / fp16 out.
+// Batch 1, K of at least 4 stages, N a multiple of 8 and the output 16-byte aligned (16-byte
+// stores), bf16 / fp16 out.
 template <bool SIMPLE>
 __global__ __launch_bounds__(256, 1) void gpf_dequant_kernel(const GemmArgs a)
 {

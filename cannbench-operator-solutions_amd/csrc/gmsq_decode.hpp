@@ -153,7 +153,7 @@ __device__ __forceinline__ bool decode_gather(const GemmArgs& a, const int r0, c
         // give up after spin_limit polls, or once any wait of the call has given up (the status
         // word: the rest of the call then leaves its tiles to the fix-up launch at once)
         if (spins >= a.epi.spin_limit ||
-            ((spins & 255) == 255 && __hip_atomic_load(a.epi.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u))
+            ((spins & 255) == 255 && (__hip_atomic_load(a.epi.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 1u)))
             return false;
         __builtin_amdgcn_s_sleep(4);
     }
@@ -182,7 +182,18 @@ __device__ __forceinline__ void decode_tile_quant(const GemmArgs& a, const int c
                 for (int k = 0; k < 4; ++k)
                     w[k] = (int)pack4_i8(rint16(act[rb][4 * k] * inv), rint16(act[rb][4 * k + 1] * inv),
                                          rint16(act[rb][4 * k + 2] * inv), rint16(act[rb][4 * k + 3] * inv));
-                *reinterpret_cast<v4i*>(e.yq + (int64_t)row * H + ocol) = w;
+                int8_t* yp = e.yq + (int64_t)row * H + ocol;
+                // H % 16 == 0 and ocol % 16 == 0: the address is aligned as y itself (a uniform choice)
+                const uintptr_t al = (uintptr_t)e.yq & 15;
+                if (al == 0) {
+                    *reinterpret_cast<v4i*>(yp) = w;
+                } else if ((al & 3) == 0) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) reinterpret_cast<int*>(yp)[k] = w[k];
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) yp[k] = (int8_t)(w[k >> 2] >> (8 * (k & 3)));
+                }
             }
             if (ct == 0 && c == 0) e.yq_scale[row] = am * kInv127;
         }
@@ -190,16 +201,18 @@ __device__ __forceinline__ void decode_tile_quant(const GemmArgs& a, const int c
 }
 
 // Requant of a finished tile once its rows' maxima are final; a wave that gives up marks the tile
-// for the fix-up launch (which redoes the whole tile) and stores nothing.
+// for the fix-up launch (which redoes the whole tile) and stores nothing.  no_wait: the tile is
+// left to the fix-up launch without waiting (status bit 1 instead of the timeout bit 0, so the
+// other waits of the call still wait).
 __device__ __forceinline__ void decode_finish(const GemmArgs& a, const int g, const int ct, const int r0, const int r1,
-                                              const float (&act)[2][16])
+                                              const float (&act)[2][16], const bool no_wait = false)
 {
     float am[2];
     // a negative poll limit (test hook) gives up at once
-    if (a.epi.spin_limit >= 0 && decode_gather(a, r0, r1, am)) {
+    if (!no_wait && a.epi.spin_limit >= 0 && decode_gather(a, r0, r1, am)) {
         decode_tile_quant(a, ct, r0, r1, act, am);
     } else if ((threadIdx.x & 63) == 0) {
-        __hip_atomic_fetch_or(a.epi.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_or(a.epi.status, no_wait ? 2u : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(a.epi.redo + g * a.ntiles + ct, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
@@ -211,13 +224,21 @@ __device__ __forceinline__ void decode_finish(const GemmArgs& a, const int g, co
 // column tiles are drawn together, so they finish together: each tile publishes its row maxima
 // into the self-validating slots as soon as its product is done, and its requant is deferred until
 // the workgroup's next tile is done, by which time the expert's other column tiles have normally
-// published; the deferred activations wait in LDS.  No tile waits before publishing, so every
-// drawn tile publishes and the waits cannot form a cycle.
+// published; the deferred activations wait in LDS.
+//
+// Progress.  The next ticket is drawn when a tile starts (its latency hides under the tile), so
+// while a workgroup waits for its deferred tile P, it holds one drawn ticket D it has not started.
+// Tickets are in expert order and a workgroup's D comes after its P, so a workgroup that waits on
+// expert g depends only on workgroups whose unstarted D lies in expert g, and those wait on
+// experts no later than g.  Along a chain of waits the experts never increase, so a cycle needs a
+// workgroup whose own D lies in its own P's expert (possible only with few workgroups, e.g. a
+// partly resident grid).  Such a workgroup does not wait: it leaves P to the fix-up launch and
+// goes on to D, so the waits cannot form a cycle.
 __global__ __launch_bounds__(256, 2) void gmsq_decode_kernel(const GemmArgs a)
 {
     __shared__ int red[3][4][16][64];      // partial sums handed to the wave that owns them (48 KiB)
     __shared__ float park[4][4][8][2][16]; // the deferred tile's activations (lanes c < 8; 16 KiB)
-    __shared__ u32 next_t;
+    __shared__ u32 next_t, pend_t;
     const int ntl = a.ntiles;
     const int count = a.gt.n_groups * ntl;
     u32* ticket = a.epi.status + 16;  // the ticket lives in the status block, after the word
@@ -242,12 +263,18 @@ __global__ __launch_bounds__(256, 2) void gmsq_decode_kernel(const GemmArgs a)
             decode_tile_act(a, g, ct, r0, r1, red, act, rmax);
             decode_publish(a, ct, r0, r1, rmax);
             if (pg >= 0) {
+                // the ticket drawn at this tile's start (returned by now) decides whether waiting
+                // for the deferred tile could wait for this workgroup itself
+                if (threadIdx.x == 0) pend_t = nt_pending;
+                __syncthreads();
+                const int pend = (int)pend_t;
+                const bool self_dep = pend < count && pend / ntl == pg;
                 float pact[2][16];
 #pragma unroll
                 for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
                     for (int j = 0; j < 16; ++j) pact[rb][j] = c < 8 ? park[wave][q][c & 7][rb][j] : 0.0f;
-                decode_finish(a, pg, pct, pr0, pr1, pact);
+                decode_finish(a, pg, pct, pr0, pr1, pact, self_dep);
             }
             if (c < 8) {
 #pragma unroll

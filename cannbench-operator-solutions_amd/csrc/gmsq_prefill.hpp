@@ -600,11 +600,47 @@ __device__ __forceinline__ u32 pf_wait(const EpiArgs& e, u32* counter, const u32
     if (e.spin_limit < 0) return 0u;
     for (int spins = 0; __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target; ++spins) {
         if (spins >= e.spin_limit ||
-            ((spins & 255) == 0 && __hip_atomic_load(e.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u))
+            ((spins & 255) == 0 && (__hip_atomic_load(e.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 1u)))
             return 0u;
         __builtin_amdgcn_s_sleep(8);
     }
+    // the counter reached its target: the row maxima published before those arrivals (release) are
+    // visible to this thread, and through the barrier that follows to the whole workgroup
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     return 1u;
+}
+
+// Publishing side of the exchange, executed by every thread after its row-maximum atomics and
+// followed by a barrier, after which thread 0 adds the workgroup's arrival (pf_arrive).  The maxima
+// and the counters are touched only by agent-scope atomics, which gfx950 performs at the device's
+// coherence point, beyond the XCD's non-coherent L2; `s_waitcnt vmcnt(0)` returns once every vector
+// memory operation of the wave has completed, its returning and non-returning atomics included,
+// so after each wave's wait and the barrier, every maximum of the tile is performed before the
+// arrival is issued.  The waiting side reads the counter and the maxima with agent-scope atomic
+// loads and takes an agent-scope acquire fence once the count is complete (pf_wait).
+// A release written in the memory model instead (a release fence per wave and a release add)
+// compiles to `buffer_wbl2 sc1`, a write-back of the XCD's whole L2, five times per tile: measured
+// 4.06 -> 5.14 ms per prefill call.  The wait also drains the next tile's stage DMAs, which the
+// K loop's first wait relies on.
+__device__ __forceinline__ void pf_release_maxima() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ void pf_arrive(u32* counter)
+{
+    __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Four int8 values of one row (consecutive columns) at a dword offset of y: one dword store, or
+// four byte stores when y itself is not 4-byte aligned (H % 16 == 0 keeps every row and column
+// offset a multiple of 4, so the choice is uniform).
+__device__ __forceinline__ void pf_store4(const u32 v, const __amdgpu_buffer_rsrc_t yr, const uint32_t off, const bool bytes)
+{
+    if (bytes) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(v >> (8 * i)), yr, off == 0x80000000u ? off : off + i, 0, 0);
+    } else {
+        __builtin_amdgcn_raw_buffer_store_b32((int)v, yr, off, 0, 0);
+    }
 }
 
 // One persistent GMSQ tile after its K loop: everything from the SwiGLU to the int8 stores.
@@ -707,11 +743,11 @@ __device__ __forceinline__ void pf_epilogue(const GemmArgs& a, uint8_t* smem, v1
             const u32 m0v = __float_as_uint(rm_l[tid]), m1v = __float_as_uint(rm_l[256 + tid]);
             __hip_atomic_fetch_max(e.amax + m0 + tid, m0v > m1v ? m0v : m1v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        // 2. exchange: every row maximum of this tile has completed before the arrival count
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // 2. exchange: every row maximum of this tile is released before the arrival count
+        pf_release_maxima();
         __syncthreads();
         if (tid == 0) {
-            __hip_atomic_fetch_add(e.arrive + arr_idx, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            pf_arrive(e.arrive + arr_idx);
             const u32 ok = pf_wait(e, e.arrive + arr_idx, arr_target);
             if (!ok) {
                 // this tile's y waits for the fix-up launch
@@ -764,7 +800,7 @@ __device__ __forceinline__ void pf_epilogue(const GemmArgs& a, uint8_t* smem, v1
                 const u32 y = (qi & 1) ? __builtin_amdgcn_perm(pz, z, 0x03070105u) : __builtin_amdgcn_perm(pz, z, 0x06020400u);
                 const int64_t col = (int64_t)nt * 128 + wn * 64 + j * 32 + (c & ~3);
                 const uint32_t off = col < H ? (uint32_t)((row + qi) * H + col) : 0x80000000u;
-                __builtin_amdgcn_raw_buffer_store_b32((int)y, yr, off, 0, 0);
+                pf_store4(y, yr, off, ((uintptr_t)e.yq & 3) != 0);
             }
         }
     }
@@ -850,11 +886,11 @@ __device__ __forceinline__ void pf_publish(const GemmArgs& a, uint8_t* smem, v16
         const u32 m0v = __float_as_uint(rm_l[tid]), m1v = __float_as_uint(rm_l[256 + tid]);
         __hip_atomic_fetch_max(e.amax + t.m0 + tid, m0v > m1v ? m0v : m1v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    // every row maximum of this tile has completed before the arrival (this also drains the next
+    // every row maximum of this tile is released before the arrival (this also drains the next
     // tile's first stages, so its loop starts without a vmcnt wait)
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    pf_release_maxima();
     __syncthreads();
-    if (tid == 0) __hip_atomic_fetch_add(e.arrive + t.mt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) pf_arrive(e.arrive + t.mt);
 #pragma unroll
     for (int fm = 0; fm < 4; ++fm)
 #pragma unroll
@@ -966,7 +1002,8 @@ struct PfDefer {
                 const uint32_t roff = (uint32_t)((64 * fm + 8 * q) * H);  // rows below slice (0, 0)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
-                    __builtin_amdgcn_raw_buffer_store_b32((int)quad_bytes(fm, q, j, inv4), yr, ybase[j] + roff, 0, 0);
+                    pf_store4(quad_bytes(fm, q, j, inv4), yr, ybase[j] == 0x80000000u ? ybase[j] : ybase[j] + roff,
+                              ((uintptr_t)e.yq & 3) != 0);
             }
         }
     }

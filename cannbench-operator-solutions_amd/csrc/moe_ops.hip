@@ -153,8 +153,9 @@ static void launch_gemm(GemmArgs& a, const int64_t* gl, int64_t E, int64_t batch
     const int pg = persistent_grid();
     if constexpr (EPI == EPI_DEQUANT) {
         // the four-wave ring core with a continuous stage stream (K of at least 4 stages) and
-        // 8-byte stores of 4 columns (N a multiple of 4; 16 bytes of 8 columns with N a multiple of 8)
-        if (batch == 1 && pg > 0 && a.K >= 4 * PfCfg::BK && Ncols % 4 == 0 && 256 * Ncols * 2 < 0x7fffffffLL) {
+        // 16-byte stores of 8 columns (N a multiple of 8, the output 16-byte aligned)
+        if (batch == 1 && pg > 0 && a.K >= 4 * PfCfg::BK && Ncols % 8 == 0 && aligned(a.epi.out, 16) &&
+            256 * Ncols * 2 < 0x7fffffffLL) {
             const EpiArgs& e = a.epi;
             const bool simple = !e.has_offset && e.bias_kind == BIAS_NONE && e.out_bf16;
             const void* kern = simple ? (const void*)gpf_dequant_kernel<true> : (const void*)gpf_dequant_kernel<false>;
@@ -281,7 +282,8 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
     // a test that turns the persistent launches off also takes the two-pass path here: the path
     // taken when the fused kernels' grids cannot all be resident
     const bool fused = g_overrides.persistent_grid >= 0;
-    if (fused && fast && a.gt.max_rows > kSkinnyMaxRows && aligned(y, 4)) {
+    if (fused && fast && a.gt.max_rows > kSkinnyMaxRows) {
+        // (y at any alignment: the stores narrow to bytes when y is not 4-byte aligned)
         // prefill-shaped groups: the persistent GEMM with the requant fused
         const int cus = device_cus();
         const int grid = (ntl == 16 && cus >= 256) ? 256 : (cus / ntl) * ntl;
@@ -313,7 +315,8 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
             return check_launch();
         }
     }
-    if (fused && fast && a.gt.max_rows <= kSkinnyMaxRows && aligned(y, 16)) {
+    if (fused && fast && a.gt.max_rows <= kSkinnyMaxRows) {
+        // (y at any alignment: 16-byte, dword or byte stores by the alignment of y)
         // decode-shaped groups: weight streaming with the requant fused (per-expert exchange), on a
         // persistent grid of two workgroups per CU drawing tiles from one ticket in expert order
         const int cus = device_cus();
@@ -323,6 +326,7 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
             resident = 0;
         const int64_t tiles = E * ntl;
         int grid = (resident < 2 ? resident : 2) * cus;
+        if (g_overrides.persistent_grid > 0 && resident >= 1) grid = g_overrides.persistent_grid;  // test hook
         if (grid > tiles) grid = (int)tiles;
         if (grid >= 1) {
             a.ntiles = ntl;

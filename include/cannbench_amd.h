@@ -159,11 +159,14 @@ int cb_grouped_matmul_swiglu_quant_gather(const int8_t* x, int64_t x_rows, const
 
 /*
  * Diagnostics (no reference counterpart): the status word a GroupedMatmulSwigluQuant call left in
- * `workspace` (the same M, N, E).  0: every row-maximum exchange completed in time.  1: some
- * exchange wait gave up (its workgroups were not all resident together within the poll limit);
- * the tiles concerned were recomputed by the fix-up launch with the final row maxima, so the
- * outputs are right either way and only the time was lost.  Synchronises `stream`, so it is meant
- * for tests and debug runs, not the hot loop.
+ * `workspace` (the same M, N, E).  0: every row-maximum exchange completed in time.  Bit 0: some
+ * exchange wait gave up (its workgroups were not all resident together within the poll limit).
+ * Bit 1: a decode-shaped tile was left to the fix-up launch without waiting, because waiting could
+ * have depended on the waiting workgroup itself (only with few workgroups, e.g. a forced small
+ * grid).  Either way the tiles concerned were recomputed by the fix-up launch with the final row
+ * maxima, so the outputs are right and only time was lost.  Synchronises `stream`, so it is meant
+ * for tests and debug runs, not the hot loop.  The status of cb_grouped_matmul_swiglu_quant_noalloc
+ * calls is not readable: it lives in the library's hidden scratch array.
  */
 int cb_grouped_matmul_swiglu_quant_status(const void* workspace, int64_t M, int64_t N, int64_t E,
                                           uint32_t* status, void* stream);
@@ -178,7 +181,8 @@ int cb_grouped_matmul_swiglu_quant_status(const void* workspace, int64_t M, int6
  * workspace would exceed 4 MiB return CB_ERR_SCRATCH_LIMIT (M = 131072 rows with N = 4096 and
  * E = 256 need about 0.7 MiB; the limit is reached near M = 979000).  Every call on one GPU shares
  * that GPU's array: calls that may overlap on one device (different streams, threads or
- * processes) race and must be ordered by the caller.
+ * processes) race and must be ordered by the caller.  The exchange status word (see
+ * cb_grouped_matmul_swiglu_quant_status) is kept in that array and cannot be queried.
  */
 int cb_grouped_matmul_swiglu_quant_noalloc(const int8_t* x, const int8_t* weight, const float* weight_scale,
                                            const float* x_scale, const int64_t* group_list, int64_t group_len,
@@ -188,8 +192,9 @@ int cb_grouped_matmul_swiglu_quant_noalloc(const int8_t* x, const int8_t* weight
 /*
  * Test hook (no reference counterpart; for this library's tests only).  Overrides for the calling
  * thread's later launches, kept until changed; 0 restores each default:
- *   persistent_grid      workgroups of the persistent dequant / int32 GEMM (default: the CU count;
- *                        a small grid makes every workgroup walk many tiles); < 0 turns that
+ *   persistent_grid      workgroups of the persistent dequant / int32 GEMM and of the decode-shaped
+ *                        GroupedMatmulSwigluQuant kernel (default: the CU count, two per CU for
+ *                        decode; a small grid makes every workgroup walk many tiles); < 0 turns that
  *                        persistent launch off, and GroupedMatmulSwigluQuant then takes its
  *                        two-pass path (the one it takes when its fused grid cannot be resident).
  *   exchange_spin_limit  polls of the GroupedMatmulSwigluQuant row-maximum exchange before a tile

@@ -1,7 +1,7 @@
 """cb_grouped_matmul_swiglu_quant_noalloc (no workspace argument, no allocation: the library's fixed
 per-GPU scratch array) against cb_grouped_matmul_swiglu_quant with a caller workspace, bit for
 bit, on consecutive calls that reuse the scratch (the second one smaller), for prefill-shaped and
-decode-shaped groups; and the size limit's status."""
+decode-shaped groups; the fix-up path through the scratch; and the size limit's status."""
 import numpy as np
 import pytest
 import torch
@@ -48,6 +48,22 @@ def test_noalloc_matches_workspace_entry(cb, first, second):
         y0, ys0 = cb.grouped_matmul_swiglu_quant(x, w, ws, xs, gl)
         y1, ys1 = _noalloc(cb, x, w, ws, xs, gl)
         torch.cuda.synchronize()
+        assert torch.equal(y0, y1), counts
+        assert torch.equal(ys0, ys1), counts
+
+
+def test_noalloc_fixup_path(cb, overrides):
+    """Every exchange wait gives up at once (test hook), so the fix-up launches recompute every tile
+    from the marks and row maxima held in the scratch array: the outputs still equal the workspace
+    entry point's normal run, for prefill- and decode-shaped groups."""
+    for counts, K, N in (([700, 0, 1300, 90], 512, 4096), ([5, 0, 17, 32, 1, 9] * 8, 448, 4096)):
+        x, w, ws, xs, gl = _inputs(counts, K, N, 7 * sum(counts) + K)
+        y0, ys0 = cb.grouped_matmul_swiglu_quant(x, w, ws, xs, gl)
+        torch.cuda.synchronize()
+        overrides(exchange_spin_limit=-1)
+        y1, ys1 = _noalloc(cb, x, w, ws, xs, gl)
+        torch.cuda.synchronize()
+        overrides()
         assert torch.equal(y0, y1), counts
         assert torch.equal(ys0, ys1), counts
 
