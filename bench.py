@@ -12,6 +12,7 @@ by a 512 MB flush write outside the events.
 
 A step is one operator call over one batch of synthetic input.  Usage:
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only prefill,decode,...] [--no-cpu]
+    python bench.py --power prefill,decode,... [--seconds S] [--lib variant.so]   (power / clock samples)
 """
 import argparse
 import importlib
@@ -468,6 +469,100 @@ def cpu_baseline_decode(d, budget_s=8.0):
                       f"decode config, {t_total:.1f} s"}
 
 
+def power_workload(name, dev):
+    """(label, fn) of one operator call for the --power mode: the bench's own inputs of each workload,
+    and the light / heavy expert subsets of the prefill routing (experts with at most / more than 256
+    rows, their rows gathered into a contiguous problem)."""
+    if name in ("prefill", "heavy", "light"):
+        d = cfgs.make_gmsq_prefill(dev)
+        if name != "prefill":
+            cnt = np.diff([0] + d["group_list"])
+            sel = np.nonzero(cnt > 256 if name == "heavy" else cnt <= 256)[0]
+            starts = np.concatenate([[0], np.cumsum(cnt)[:-1]])
+            rows = torch.from_numpy(np.concatenate([np.arange(starts[e], starts[e] + cnt[e]) for e in sel])).to(dev)
+            es = torch.from_numpy(sel).to(dev)
+            d = {"x": d["x"].index_select(0, rows), "weight": d["weight"].index_select(0, es),
+                 "weight_scale": d["weight_scale"].index_select(0, es), "x_scale": d["x_scale"].index_select(0, rows),
+                 "group_list": [int(v) for v in np.cumsum(cnt[sel])]}
+            torch.cuda.empty_cache()
+        return (f"gmsq_{name}", lambda: cb.grouped_matmul_swiglu_quant(d["x"], d["weight"], d["weight_scale"],
+                                                                        d["x_scale"], d["group_list"]))
+    if name == "decode":
+        d = cfgs.make_gmsq_decode(dev, with_down=False)
+        return "gmsq_decode", lambda: cb.grouped_matmul_swiglu_quant(d["x"], d["weight"], d["weight_scale"],
+                                                                      d["x_scale"], d["group_list"])
+    if name == "qmm":
+        d = cfgs.make_qmm(dev)
+        return "qmm", lambda: cb.quant_matmul(d["x1"], d["x2"], d["scale"], pertoken_scale=d["pertoken_scale"],
+                                              output_dtype="bfloat16")
+    if name == "down_prefill":
+        gl = cfgs.cumsum_list(cfgs.zipf_group_counts(131072, 256))
+        r = cfgs.streams(41, 4)
+        x = cfgs.rand_i8((131072, 2048), dev, r[0])
+        xs = cfgs.rand_uniform((131072,), 0.005, 0.02, dev, r[1])
+        w = cfgs.rand_i8((256, 2048, 7168), dev, r[2])
+        ws = cfgs.rand_uniform((256, 7168), 0.001, 0.01, dev, r[3])
+        return "down_proj_prefill", lambda: cb.grouped_matmul_quant(x, w, ws, xs, gl)
+    if name == "ardq":
+        d = cfgs.make_ardq(dev)
+        return "ardq", lambda: cb.add_rms_norm_dynamic_quant(d["x1"], d["x2"], d["gamma"], d["epsilon"])
+    if name == "dqsq":
+        d = cfgs.make_dqsq(dev)
+        return "dqsq", lambda: cb.dequant_swiglu_quant(d["x"], d["weight_scale"], d["activation_scale"])
+    if name == "mfma_probe":
+        import ctypes
+        lib = L.load()
+        sink = torch.zeros(8 * 256, dtype=torch.int32, device=dev)
+        ops = ctypes.c_int64(0)
+        return "mfma_probe", lambda: lib.cb_probe_mfma_i8(2000, sink.data_ptr(), sink.numel(), ctypes.byref(ops),
+                                                          torch.cuda.current_stream().cuda_stream)
+    raise SystemExit(f"bench.py --power: unknown workload {name}")
+
+
+def power_mode(names, seconds, dev):
+    """Loops each workload for `seconds` while `amd-smi metric --power --clock` is sampled about once
+    a second (after a 2 s settling time), and prints one JSON line per workload: the median socket
+    power and GFX clock over the samples and the mean time per call."""
+    import re
+    import subprocess
+    import threading
+    for name in names:
+        label, fn = power_workload(name, dev)
+        fn()
+        torch.cuda.synchronize()
+        samples, stop = [], threading.Event()
+
+        def sample():
+            time.sleep(2.0)
+            while not stop.is_set():
+                r = subprocess.run(["amd-smi", "metric", "--power", "--clock"], capture_output=True, text=True)
+                pw = re.search(r"SOCKET_POWER:\s*([0-9.]+)", r.stdout)
+                k = r.stdout.find("GFX")  # the first CLK line after it is the GFX clock
+                gfx = re.search(r"\bCLK:\s*([0-9.]+)", r.stdout[k if k >= 0 else 0:])
+                if pw and gfx:
+                    samples.append((float(pw.group(1)), float(gfx.group(1))))
+                time.sleep(1.0)
+
+        th = threading.Thread(target=sample, daemon=True)
+        th.start()
+        t0, n = time.perf_counter(), 0
+        while time.perf_counter() - t0 < seconds:
+            for _ in range(10):
+                fn()
+            torch.cuda.synchronize()
+            n += 10
+        ms = (time.perf_counter() - t0) * 1e3 / n
+        stop.set()
+        th.join()
+        pw = [p for p, _ in samples]
+        ck = [c for _, c in samples]
+        print(json.dumps({"power_mode": label, "library": L.LIB_PATH, "ms_per_call": round(ms, 4), "calls": n,
+                          "samples": len(samples),
+                          "socket_power_w_median": float(np.median(pw)) if pw else None,
+                          "gfx_clock_mhz_median": float(np.median(ck)) if ck else None,
+                          "gfx_clock_mhz_range": [min(ck), max(ck)] if ck else None}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -479,7 +574,16 @@ def main():
                     help="comma list of prefill, gather and down_prefill (need prefill), decode, ardq, qmm, "
                          "routing, gmm, vendor, copy")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--power", default=None,
+                    help="comma list of workloads (prefill, heavy, light, decode, qmm, down_prefill, ardq, dqsq, "
+                         "mfma_probe): loop each for --seconds while sampling socket power and GFX clock with "
+                         "amd-smi, print one JSON line each, and exit (no bench line)")
+    ap.add_argument("--seconds", type=float, default=8.0)
+    ap.add_argument("--lib", default=None, help="operator library to load instead of the in-tree build "
+                                                "(a variant built from a patched source tree, for --power)")
     args = ap.parse_args()
+    if args.lib:
+        L.LIB_PATH = os.path.abspath(args.lib)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the operators are single-device; expert "
               "parallelism across GPUs is a design note, not a measured path). Use --gpus 1.", file=sys.stderr)
@@ -489,6 +593,9 @@ def main():
         sys.exit(2)
     dev = "cuda:0"
     torch.cuda.set_device(0)
+    if args.power:
+        power_mode(args.power.split(","), args.seconds, dev)
+        return
     only = set(args.only.split(","))
     keep = {}
     out = {"metric": METRIC, "value": None, "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
