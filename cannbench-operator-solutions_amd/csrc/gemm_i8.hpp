@@ -211,14 +211,48 @@ __device__ __forceinline__ void set_comp(uint4& v, int i, u32 x)
     else v.w = x;
 }
 
+// The activation operand of a skinny row block: a wave-uniform buffer resource and this lane's row
+// offset in it (kSkOff: the row reads zeros).  A resource per lane (one per row) would make the
+// compiler wrap every activation load in a readfirstlane loop over the distinct resources, and
+// the wait for such a load drains every load issued before it.
+constexpr uint32_t kSkOff = 0x80000000u;
+struct SkinnyRow {
+    __amdgpu_buffer_rsrc_t res;
+    uint32_t off;   // row start of this lane (kSkOff: none)
+    uint32_t k;     // row length K in bytes
+};
+
+// Row block starting at row mb of a group ending at r1; lane c takes row mb + c.  boff: the batch
+// offset of x (dense QuantMatmul).  Gathered rows address all of x through the row index
+// (x_rows * K < 2^31, checked on the host); contiguous rows a 16-row window from mb.
+__device__ __forceinline__ SkinnyRow skinny_row(const GemmArgs& a, const int64_t boff, const int mb, const int r1,
+                                                const int c)
+{
+    SkinnyRow s;
+    const int64_t K = a.K;
+    s.k = (uint32_t)K;
+    const int arow = mb + c;
+    if (a.row_index) {
+        const int srow = arow < r1 ? src_row(a, arow) : -1;
+        s.res = make_rsrc(a.x + boff, (uint32_t)(a.x_rows * K));
+        s.off = srow >= 0 ? (uint32_t)srow * (uint32_t)K : kSkOff;
+    } else {
+        const int nrow = r1 - mb < 16 ? r1 - mb : 16;
+        s.res = make_rsrc(a.x + boff + (int64_t)mb * K, (uint32_t)((int64_t)nrow * K));
+        s.off = arow < r1 ? (uint32_t)c * (uint32_t)K : kSkOff;
+    }
+    return s;
+}
+
 // One 64-deep chunk of a skinny tile: the lane's activation operand (first, so waiting for it never
-// waits for weights issued later) and 16 weight rows; rows past K (and rows outside the activation
-// resource) read as zeros.
-__device__ __forceinline__ void skinny_load_chunk(__amdgpu_buffer_rsrc_t xres, __amdgpu_buffer_rsrc_t wres,
+// waits for weights issued later) and 16 weight rows; k past K (and rows outside the group) read as
+// zeros.
+__device__ __forceinline__ void skinny_load_chunk(const SkinnyRow& xr, __amdgpu_buffer_rsrc_t wres,
                                                   const uint32_t lane_off, const uint32_t n, const int q,
                                                   const int kc, uint4 (&R)[16], v4i& A)
 {
-    A = __builtin_amdgcn_raw_buffer_load_b128(xres, (uint32_t)(kc * 64 + q * 16), 0, 0);
+    const uint32_t k = (uint32_t)(kc * 64 + q * 16);
+    A = __builtin_amdgcn_raw_buffer_load_b128(xr.res, xr.off != kSkOff && k < xr.k ? xr.off + k : kSkOff, 0, 0);
     const uint32_t kofs = (uint32_t)(kc * 64) * n;
 #pragma unroll
     for (int i = 0; i < 16; ++i) R[i] = buf_load16(wres, lane_off + kofs + (uint32_t)i * n);
@@ -342,14 +376,9 @@ __global__ __launch_bounds__(256, 2) void skinny_kernel(const GemmArgs a)
 #pragma unroll
         for (int j = 0; j < 16; ++j) acc[j] = v4i{0, 0, 0, 0};
 
-        const int arow = mb + c;
-        const int asrc = arow < r1 ? src_row(a, arow) : -1;
-        const bool arow_ok = asrc >= 0;
-        // activation row of this lane through a buffer resource: rows past the group (or gathered
-        // from outside x) and k past K read as zeros without a branch, so the activation load joins
-        // its chunk's weight loads
-        const __amdgpu_buffer_rsrc_t xres =
-            make_rsrc(a.x + b * a.x_bstride + (int64_t)(arow_ok ? asrc : 0) * K, arow_ok ? (uint32_t)K : 0u);
+        // activation row of this lane: rows past the group (or gathered from outside x) and k past
+        // K read as zeros without a branch, so the activation load joins its chunk's weight loads
+        const SkinnyRow xres = skinny_row(a, b * a.x_bstride, mb, r1, c);
 
         // one chunk = the activation operand (first, so waiting for it never waits for weights
         // issued later) and 16 weight rows

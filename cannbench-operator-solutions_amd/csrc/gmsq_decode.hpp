@@ -47,16 +47,20 @@ __device__ __forceinline__ void decode_tile_act(const GemmArgs& a, const int g, 
         v4i acc[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) acc[j] = v4i{0, 0, 0, 0};
-        const int arow = mb + c;
-        const int asrc = arow < r1 ? src_row(a, arow) : -1;
-        const bool arow_ok = asrc >= 0;
-        const __amdgpu_buffer_rsrc_t xres =
-            make_rsrc(a.x + (int64_t)(arow_ok ? asrc : 0) * K, arow_ok ? (uint32_t)K : 0u);
-        for (int kc = wave; kc < nch; kc += 4) {
-            uint4 R[16];
-            v4i A;
-            skinny_load_chunk(xres, wres, lane_off, (uint32_t)N, q, kc, R, A);
-            skinny_mma_chunk(R, A, acc);
+        const SkinnyRow xres = skinny_row(a, 0, mb, r1, c);
+        // wave w multiplies chunks w, w + 4, ...; two chunks in flight per wave (register double
+        // buffering): the load of chunk kc + 8 goes out as soon as chunk kc is multiplied.  Chunks
+        // past K read zeros through both resources (their MFMAs add nothing), so the loop needs no
+        // branch around a load.
+        uint4 R0[16], R1[16];
+        v4i A0, A1;
+        skinny_load_chunk(xres, wres, lane_off, (uint32_t)N, q, wave, R0, A0);
+        skinny_load_chunk(xres, wres, lane_off, (uint32_t)N, q, wave + 4, R1, A1);
+        for (int kc = wave; kc < nch; kc += 8) {
+            skinny_mma_chunk(R0, A0, acc);
+            skinny_load_chunk(xres, wres, lane_off, (uint32_t)N, q, kc + 8, R0, A0);
+            skinny_mma_chunk(R1, A1, acc);
+            skinny_load_chunk(xres, wres, lane_off, (uint32_t)N, q, kc + 12, R1, A1);
         }
         // exact cross-wave K reduction: wave w keeps accumulator row w
 #pragma unroll
@@ -234,7 +238,7 @@ __device__ __forceinline__ void decode_finish(const GemmArgs& a, const int g, co
 // workgroup whose own D lies in its own P's expert (possible only with few workgroups, e.g. a
 // partly resident grid).  Such a workgroup does not wait: it leaves P to the fix-up launch and
 // goes on to D, so the waits cannot form a cycle.
-__global__ __launch_bounds__(256, 2) void gmsq_decode_kernel(const GemmArgs a)
+__global__ __launch_bounds__(256, 1) void gmsq_decode_kernel(const GemmArgs a)
 {
     __shared__ int red[3][4][16][64];      // partial sums handed to the wave that owns them (48 KiB)
     __shared__ float park[4][4][8][2][16]; // the deferred tile's activations (lanes c < 8; 16 KiB)
@@ -303,7 +307,7 @@ __global__ __launch_bounds__(256, 2) void gmsq_decode_kernel(const GemmArgs a)
 }
 
 // Fix-up launch: tiles marked in redo[g * ntiles + ct], recomputed with the final row maxima.
-__global__ __launch_bounds__(256, 2) void gmsq_decode_fixup_kernel(const GemmArgs a)
+__global__ __launch_bounds__(256, 1) void gmsq_decode_fixup_kernel(const GemmArgs a)
 {
     __shared__ int red[3][4][16][64];
     // no wait timed out in the main launch (status word 0): nothing is marked

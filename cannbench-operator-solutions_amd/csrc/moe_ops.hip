@@ -318,14 +318,15 @@ static int gmsq_impl(const int8_t* x, int64_t x_rows, const int32_t* row_index, 
     if (fused && fast && a.gt.max_rows <= kSkinnyMaxRows) {
         // (y at any alignment: 16-byte, dword or byte stores by the alignment of y)
         // decode-shaped groups: weight streaming with the requant fused (per-expert exchange), on a
-        // persistent grid of two workgroups per CU drawing tiles from one ticket in expert order
+        // persistent grid of one workgroup per CU (each wave keeps two weight chunks in flight in
+        // its registers) drawing tiles from one ticket in expert order
         const int cus = device_cus();
         int resident = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, (const void*)gmsq_decode_kernel, 256, 0) !=
             hipSuccess)
             resident = 0;
         const int64_t tiles = E * ntl;
-        int grid = (resident < 2 ? resident : 2) * cus;
+        int grid = (resident < 1 ? resident : 1) * cus;
         if (g_overrides.persistent_grid > 0 && resident >= 1) grid = g_overrides.persistent_grid;  // test hook
         if (grid > tiles) grid = (int)tiles;
         if (grid >= 1) {

@@ -193,8 +193,8 @@ int cb_grouped_matmul_swiglu_quant_noalloc(const int8_t* x, const int8_t* weight
  * Test hook (no reference counterpart; for this library's tests only).  Overrides for the calling
  * thread's later launches, kept until changed; 0 restores each default:
  *   persistent_grid      workgroups of the persistent dequant / int32 GEMM and of the decode-shaped
- *                        GroupedMatmulSwigluQuant kernel (default: the CU count, two per CU for
- *                        decode; a small grid makes every workgroup walk many tiles); < 0 turns that
+ *                        GroupedMatmulSwigluQuant kernel (default: the CU count; a small grid makes
+ *                        every workgroup walk many tiles); < 0 turns that
  *                        persistent launch off, and GroupedMatmulSwigluQuant then takes its
  *                        two-pass path (the one it takes when its fused grid cannot be resident).
  *   exchange_spin_limit  polls of the GroupedMatmulSwigluQuant row-maximum exchange before a tile
