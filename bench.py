@@ -8,7 +8,7 @@ dense QuantMatmul and the routing operators (gating, re-routing, finalize, Dequa
 each with its own roofline figure, plus CPU baselines (the C oracle on bounded samples of the
 prefill and decode experts, on the host cores).  Every time is the median over the timed calls of
 HIP events around each call; configs 2 and 3 (whose inputs would fit the 256 MB MALL) are preceded
-by a 512 MB flush write outside the events.
+by a 512 MB flush (a write, then a read) outside the events.
 
 A step is one operator call over one batch of synthetic input.  Usage:
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only prefill,decode,...] [--no-cpu]
@@ -62,16 +62,20 @@ FLUSH_BYTES = 512 << 20  # twice the 256 MB MALL: a write of it evicts every cac
 
 
 class Flush:
-    """A 512 MB device write issued before a timed call, outside its events, so that the call's
-    inputs come from HBM rather than the 256 MB MALL or the L2s (SURVEY 8(d) for configs 2 and 3)."""
+    """A 512 MB device write, then a read of the same buffer, issued before a timed call and outside
+    its events, so that the call's inputs come from HBM rather than the 256 MB MALL or the L2s
+    (the inputs of configs 2 and 3 would fit the MALL).  The read leaves the caches holding clean lines, so the timed
+    call does not also pay for writing back the flush's dirty ones."""
 
     def __init__(self, dev):
         self.buf = torch.empty(FLUSH_BYTES // 4, dtype=torch.int32, device=dev)
+        self.sink = torch.empty((), dtype=torch.int64, device=dev)
         self.k = 0
 
     def __call__(self):
         self.k += 1
         self.buf.fill_(self.k)
+        torch.sum(self.buf, dim=0, dtype=torch.int64, out=self.sink)
 
 
 def time_op(fn, steps, warmup, timer=None, flush=None):
