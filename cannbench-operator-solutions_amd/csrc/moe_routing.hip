@@ -7,6 +7,7 @@
 // All four are HBM-bound gather / row kernels: rows are moved with 16-byte accesses, per-row
 // reductions are wave / workgroup shuffles, and nothing is staged through host memory.
 #include <cstring>
+#include <type_traits>
 
 #include "common.hpp"
 #include "host_util.hpp"
@@ -708,11 +709,45 @@ __device__ __forceinline__ float row_reduce(float v)
     return v;
 }
 
+// Row maximum of round candidates: exp(x - max) >= 0 or the -1 sentinel.  Compared as signed
+// integers these order as the floats do (non-negative floats by their bits, -1 below them), and
+// the DPP moves fuse into v_max_i32 without the float path's canonicalising max.
+template <int CTRL>
+__device__ __forceinline__ int dpp_imax(int v)
+{
+    return max(v, __builtin_amdgcn_update_dpp((int)0x80000000, v, CTRL, 0xf, 0xf, false));
+}
+
+template <int LPR>
+__device__ __forceinline__ float row_max_candidates(float f)
+{
+    int v = __float_as_int(f);
+    v = dpp_imax<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    v = dpp_imax<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    v = dpp_imax<0x124>(v);  // row_ror 4
+    v = dpp_imax<0x128>(v);  // row_ror 8
+    if constexpr (LPR == 64) {
+        const int r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+        const int r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+        v = max(max(r0, r1), max(r2, r3));
+    }
+    return __int_as_float(v);
+}
+
 // One row per LPR lanes; lane `sub` of a row owns the EPL consecutive columns [sub*EPL, sub*EPL+EPL).
 // Each of the k rounds takes every lane's best remaining value (lowest column on ties), reduces the
-// row maximum, and lets the lowest lane holding it (hence the lowest column) emit and retire it:
-// the order of a stable descending sort.  Every lane of the wave stays active for the DPP moves.
-template <int DT, int LPR, int EPL, bool VLD>
+// row maximum, and lets the lowest lane holding it (hence the lowest column) emit it: the order of a
+// stable descending sort.  Every lane of the wave stays active for the DPP moves.
+//
+// A lane keeps its next MGT_LIST values in emission order (descending, lower column first on ties),
+// built once by insertion (MGT_LIST = k for k <= 2, else 4); a win pops the head, and only a lane whose
+// list a win empties while it still has values and rounds remain rebuilds it from the columns after
+// the one it emitted last (a wave-uniform branch, rare for MGT_LIST 4: a lane must win 4 of the k
+// rounds).  For k <= LPR the round's value and
+// column go to row lane j (the column read from the winner with ds_bpermute), and after the rounds
+// each of the first k lanes of the row divides once and stores its output; larger k store from the
+// winner in each round.
+template <int DT, int LPR, int EPL, bool VLD, int MGT_LIST>
 __global__ __launch_bounds__(256) void mgt_kernel(const void* __restrict__ x, int64_t rows, int E,
                                                   const uint8_t* __restrict__ finished, int k,
                                                   void* __restrict__ y, int32_t* __restrict__ eidx,
@@ -752,43 +787,81 @@ __global__ __launch_bounds__(256) void mgt_kernel(const void* __restrict__ x, in
 #pragma unroll
     for (int u = 0; u < EPL; ++u) {
         const bool in = live && c0 + u < E;
-        v[u] = in ? __expf(v[u] - m) : -1.0f;  // exp(x - max) >= 0: padding and retired slots sort last
+        v[u] = in ? __expf(v[u] - m) : -1.0f;  // exp(x - max) >= 0: padding sorts last
         s += in ? v[u] : 0.0f;
     }
     s = row_reduce<LPR, false>(s);
     const bool fin = live && finished && finished[r];
     const unsigned long long row_bits = LPR == 64 ? ~0ull : ((1ull << LPR) - 1) << (grp * LPR);
-    // the lane's best remaining value (lowest column on ties); only a round's winner rescans
-    float bv = v[0];
-    int bu = 0;
+    constexpr int T = EPL < MGT_LIST ? EPL : MGT_LIST;
+    float tv[T];
+    int tu[T];
+    // the lane's best T values among the slots after (lv, lu) in emission order (every slot when
+    // `all` is true_type); padding and an empty list entry are -1, below every exp(x - max) >= 0
+    auto fill = [&](auto all, const float lv, const int lu) {
 #pragma unroll
-    for (int u = 1; u < EPL; ++u)
-        if (v[u] > bv) {
-            bv = v[u];
-            bu = u;
+        for (int t = 0; t < T; ++t) {
+            tv[t] = -1.0f;
+            tu[t] = 0;
         }
-    for (int j = 0; j < k; ++j) {
-        const float mrow = row_reduce<LPR, true>(bv);
-        const unsigned long long hit = __ballot(bv == mrow) & row_bits;
-        const int w = __ffsll((long long)hit) - 1;
-        if (lane == w) {
-            if (live) {
-                st_any<DT>(y, r * k + j, bv / s);
-                eidx[r * k + j] = fin ? E : c0 + bu;
-                ridx[r * k + j] = (int32_t)((int64_t)j * rows + r);
+#pragma unroll
+        for (int u = 0; u < EPL; ++u) {
+            float x = v[u];
+            if constexpr (!decltype(all)::value) x = (v[u] < lv || (v[u] == lv && u > lu)) ? x : -1.0f;
+            bool g[T];
+#pragma unroll
+            for (int t = 0; t < T; ++t) g[t] = x > tv[t];  // strict: the lower slot stays first on ties
+#pragma unroll
+            for (int t = T - 1; t > 0; --t) {
+                tv[t] = g[t - 1] ? tv[t - 1] : (g[t] ? x : tv[t]);
+                tu[t] = g[t - 1] ? tu[t - 1] : (g[t] ? u : tu[t]);
             }
-#pragma unroll
-            for (int u = 0; u < EPL; ++u)
-                if (u == bu) v[u] = -1.0f;
-            bv = v[0];
-            bu = 0;
-#pragma unroll
-            for (int u = 1; u < EPL; ++u)
-                if (v[u] > bv) {
-                    bv = v[u];
-                    bu = u;
-                }
+            tv[0] = g[0] ? x : tv[0];
+            tu[0] = g[0] ? u : tu[0];
         }
+    };
+    fill(std::true_type{}, 0.0f, 0);
+    const int nval = live ? (E - c0 < 0 ? 0 : E - c0 < EPL ? E - c0 : EPL) : 0;
+    int npop = 0;
+    float lv = 0.0f;
+    int lu = 0;
+    const bool staged = k <= LPR;  // wave-uniform
+    float ov = 0.0f;
+    int oc = 0;
+    for (int j = 0; j < k; ++j) {
+        const float mrow = row_max_candidates<LPR>(tv[0]);
+        const unsigned long long hit = __ballot(tv[0] == mrow) & row_bits;
+        const int w = __ffsll((long long)hit) - 1;
+        const bool win = lane == w;
+        if (staged) {
+            const int col = __builtin_amdgcn_ds_bpermute(w << 2, c0 + tu[0]);
+            ov = sub == j ? mrow : ov;
+            oc = sub == j ? col : oc;
+        } else if (win && live) {
+            st_any<DT>(y, r * k + j, tv[0] / s);
+            eidx[r * k + j] = fin ? E : c0 + tu[0];
+            ridx[r * k + j] = (int32_t)((int64_t)j * rows + r);
+        }
+        if (win) {
+            lv = tv[0];
+            lu = tu[0];
+#pragma unroll
+            for (int t = 0; t + 1 < T; ++t) {
+                tv[t] = tv[t + 1];
+                tu[t] = tu[t + 1];
+            }
+            tv[T - 1] = -1.0f;
+            ++npop;
+        }
+        const bool refill = win && tv[0] < 0.0f && npop < nval && j + 1 < k;
+        if (__ballot(refill) != 0ull) {
+            if (refill) fill(std::false_type{}, lv, lu);
+        }
+    }
+    if (staged && live && sub < k) {
+        st_any<DT>(y, r * k + sub, ov / s);
+        eidx[r * k + sub] = fin ? E : oc;
+        ridx[r * k + sub] = (int32_t)((int64_t)sub * rows + r);
     }
 }
 
@@ -1012,8 +1085,17 @@ extern "C" int cb_moe_gating_top_k_softmax(const void* x, int dtype, int64_t row
     const int vw = dtype == CB_DT_FLOAT32 ? 4 : 8;
     const bool vld = E == (int64_t)lpr * epl && epl % vw == 0 && aligned(x, 16);
 #define CB_MGT(DTV, LPRV, EPLV, VLDV)                                                              \
-    hipLaunchKernelGGL((mgt_kernel<DTV, LPRV, EPLV, VLDV>), grid, block, 0, st, x, rows, (int)E, finished, \
-                       (int)k, y, expert_idx, row_idx)
+    do {                                                                                           \
+        if (k == 1)                                                                                \
+            hipLaunchKernelGGL((mgt_kernel<DTV, LPRV, EPLV, VLDV, 1>), grid, block, 0, st, x, rows, (int)E, \
+                               finished, (int)k, y, expert_idx, row_idx);                          \
+        else if (k == 2)                                                                           \
+            hipLaunchKernelGGL((mgt_kernel<DTV, LPRV, EPLV, VLDV, 2>), grid, block, 0, st, x, rows, (int)E, \
+                               finished, (int)k, y, expert_idx, row_idx);                          \
+        else                                                                                       \
+            hipLaunchKernelGGL((mgt_kernel<DTV, LPRV, EPLV, VLDV, 4>), grid, block, 0, st, x, rows, (int)E, \
+                               finished, (int)k, y, expert_idx, row_idx);                          \
+    } while (0)
 #define CB_MGT_V(DTV, LPRV, EPLV)                                                                  \
     do {                                                                                           \
         if constexpr (EPLV % ((DTV) == CB_DT_FLOAT32 ? 4 : 8) == 0) {                             \

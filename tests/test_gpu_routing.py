@@ -176,7 +176,7 @@ def test_dequant_swiglu_quant_zero_rows_and_checks(cb):
 # MoeGatingTopKSoftmax
 # ---------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
-@pytest.mark.parametrize("rows,E,k", [(4096, 256, 8), (1000, 64, 6), (77, 8, 2), (33, 2048, 16),
+@pytest.mark.parametrize("rows,E,k", [(4096, 256, 8), (2000, 256, 1), (1000, 64, 6), (77, 8, 2), (500, 256, 2), (33, 2048, 16),
                                       (9, 130, 130), (5, 1, 1), (16, 16, 16)])
 @pytest.mark.parametrize("fin", [False, True])
 def test_moe_gating_top_k_softmax(cb, orc, dt, rows, E, k, fin):
@@ -197,6 +197,31 @@ def test_moe_gating_top_k_softmax(cb, orc, dt, rows, E, k, fin):
         got = y.cpu().float().numpy()
         ref = torch.from_numpy(ry.view(np.int16)).view(TD[dt]).float().numpy()
         np.testing.assert_allclose(got, ref, rtol=1e-2, atol=1e-6)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("E,k,span", [(256, 8, 16), (256, 12, 16), (256, 16, 32), (2048, 24, 32), (130, 40, 9)])
+def test_moe_gating_one_lane_holds_the_top(cb, orc, dt, E, k, span):
+    """The k largest values of a row lie in `span` consecutive columns, i.e. one or two lanes'
+    slots, so those lanes win many rounds in a row and refill their candidate lists from the
+    columns after the last one they emitted; bf16 rounding adds ties among them."""
+    g = gen(E + k + span)
+    rows = 300
+    x = torch.randn(rows, E, generator=g)
+    start = torch.randint(0, E - span + 1, (rows,), generator=g)
+    for r in range(rows):
+        x[r, start[r]:start[r] + span] += 6.0
+    x = x.to(TD[dt])
+    y, ei, ri = cb.moe_gating_top_k_softmax(x.to(DEV), None, k)
+    torch.cuda.synchronize()
+    ry, rei, rri = orc.moe_gating_top_k_softmax(host(x, dt), dt, k, None)
+    np.testing.assert_array_equal(ei.cpu().numpy(), rei)
+    np.testing.assert_array_equal(ri.cpu().numpy(), rri)
+    if dt == "f32":
+        np.testing.assert_allclose(y.cpu().numpy(), ry, rtol=1e-5, atol=1e-9)
+    else:
+        ref = torch.from_numpy(ry.view(np.int16)).view(TD[dt]).float().numpy()
+        np.testing.assert_allclose(y.cpu().float().numpy(), ref, rtol=1e-2, atol=1e-6)
 
 
 def test_moe_gating_batched_shape(cb):
