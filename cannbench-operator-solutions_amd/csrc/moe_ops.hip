@@ -160,7 +160,9 @@ static void launch_gemm(GemmArgs& a, const int64_t* gl, int64_t E, int64_t batch
             const bool simple = !e.has_offset && e.bias_kind == BIAS_NONE && e.out_bf16;
             const void* kern = simple ? (const void*)gpf_dequant_kernel<true> : (const void*)gpf_dequant_kernel<false>;
             allow_dynamic_lds(kern, kGpfLds);
-            const dim3 grid((unsigned)(blocks < pg ? blocks : pg));
+            // the block map's valid slots are spread over each round of 256: launch the whole grid
+            const bool bm = gpf_block_map(a.gt.total_mtiles, a.ntiles);
+            const dim3 grid((unsigned)(bm || blocks > pg ? pg : blocks));
             if (simple) hipLaunchKernelGGL(gpf_dequant_kernel<true>, grid, dim3(256), kGpfLds, st, a);
             else hipLaunchKernelGGL(gpf_dequant_kernel<false>, grid, dim3(256), kGpfLds, st, a);
             return;

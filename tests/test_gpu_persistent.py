@@ -1,7 +1,7 @@
 """GPU parity of the persistent dequant / int32 GEMM (one continuous DMA stage stream per workgroup).
 
 These tests force a small grid with the library's test override, so every workgroup walks many
-tiles (the dequant GEMM on the ring core and the 8-wave int32 GEMM).  Together the cases cover an odd number of K stages (the ring rotates between tiles), K of
+tiles (the dequant GEMM on the ring core and the 8-wave int32 GEMM).  Together the cases cover an odd number of K stages (the ring rotates between tiles), both launch orders of the ring core (row tile runs; 4 x 8 tile blocks per XCD), K of
 exactly the ring's depth, K shorter than the ring (launched one tile per workgroup instead), ragged
 and empty groups, partial row and column tiles, every dequant flag, and the last tile's stages that
 fetch nothing.  The bar is the same as the non-persistent path: bit-exact against the oracle.
@@ -42,6 +42,10 @@ GMQ_CASES = [
     ([270, 40], 400, 784),
     ([520, 17, 0], 256, 512),
     ([520, 17, 0], 96, 512),
+    # 8 column tiles (the last one 248 wide) and at least 4 row tiles: the block launch order (4 row
+    # tiles x 8 column tiles per XCD and round), with a partial last band of row tiles
+    ([520, 17, 0, 700], 256, 2040),
+    ([300, 0, 45, 600, 1, 0, 33, 256, 90], 448, 4096),
 ]
 
 
