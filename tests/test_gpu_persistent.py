@@ -46,6 +46,9 @@ GMQ_CASES = [
     # tiles x 8 column tiles per XCD and round), with a partial last band of row tiles
     ([520, 17, 0, 700], 256, 2040),
     ([300, 0, 45, 600, 1, 0, 33, 256, 90], 448, 4096),
+    # N % 8 == 4 with K of at least 4 stages: the ring core's 16-byte stores need N % 8 == 0, so
+    # these take the 8-wave persistent kernel
+    ([300, 0, 45, 600], 384, 772),
 ]
 
 
@@ -108,6 +111,21 @@ def test_persistent_quant_matmul_flags(cb, orc, small_grid, variant):
     out = cb.quant_matmul(x1, x2, scale.to(DEV), **kw)
     sc_np = bits16(scale) if scale.dtype == torch.bfloat16 else scale.numpy()
     ref = orc.quant_matmul(x1.cpu().numpy(), x2.cpu().numpy(), sc_np, **okw)
+    np.testing.assert_array_equal(bits16(out).reshape(ref.shape), ref)
+
+
+@pytest.mark.parametrize("N", [772, 100])
+def test_quant_matmul_n_mod8_4(cb, orc, small_grid, N):
+    """QuantMatmul with N % 8 == 4 and K >= 256 (outside the ring core's 16-byte store gate):
+    bit-exact against the oracle on the kernel these shapes take."""
+    g = cpu_gen(N)
+    M, K = 300, 512
+    x1 = rand_i8((M, K), g)
+    x2 = rand_i8((K, N), g)
+    scale = torch.rand(N, generator=g) * 0.009 + 0.001
+    pt = torch.rand(M, generator=g) * 0.015 + 0.005
+    out = cb.quant_matmul(x1, x2, scale.to(DEV), pertoken_scale=pt.to(DEV), output_dtype="bfloat16")
+    ref = orc.quant_matmul(x1.cpu().numpy(), x2.cpu().numpy(), scale.numpy(), pertoken=pt.numpy(), out_dtype="bf16")
     np.testing.assert_array_equal(bits16(out).reshape(ref.shape), ref)
 
 
