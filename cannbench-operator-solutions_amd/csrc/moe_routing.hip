@@ -740,13 +740,12 @@ __device__ __forceinline__ float row_max_candidates(float f)
 // stable descending sort.  Every lane of the wave stays active for the DPP moves.
 //
 // A lane keeps its next MGT_LIST values in emission order (descending, lower column first on ties),
-// built once by insertion (MGT_LIST = k for k <= 2, else 4); a win pops the head, and only a lane whose
-// list a win empties while it still has values and rounds remain rebuilds it from the columns after
-// the one it emitted last (a wave-uniform branch, rare for MGT_LIST 4: a lane must win 4 of the k
-// rounds).  For k <= LPR the round's value and
-// column go to row lane j (the column read from the winner with ds_bpermute), and after the rounds
-// each of the first k lanes of the row divides once and stores its output; larger k store from the
-// winner in each round.
+// built once by insertion (MGT_LIST = k for k <= 2, else 4).  A win pops the head; a lane whose
+// list a win empties rebuilds it from the columns after the one it emitted last (a wave-uniform
+// branch, rare for MGT_LIST 4: a lane must win 4 of the k rounds), except after the last round.
+// For k <= LPR the round's value and column go to row lane j (the column read from the winner
+// with ds_bpermute), and after the rounds each of the first k lanes of the row divides once and
+// stores its output; larger k store from the winner in each round.
 template <int DT, int LPR, int EPL, bool VLD, int MGT_LIST>
 __global__ __launch_bounds__(256) void mgt_kernel(const void* __restrict__ x, int64_t rows, int E,
                                                   const uint8_t* __restrict__ finished, int k,
@@ -792,7 +791,6 @@ __global__ __launch_bounds__(256) void mgt_kernel(const void* __restrict__ x, in
     }
     s = row_reduce<LPR, false>(s);
     const bool fin = live && finished && finished[r];
-    const unsigned long long row_bits = LPR == 64 ? ~0ull : ((1ull << LPR) - 1) << (grp * LPR);
     constexpr int T = EPL < MGT_LIST ? EPL : MGT_LIST;
     float tv[T];
     int tu[T];
@@ -821,27 +819,17 @@ __global__ __launch_bounds__(256) void mgt_kernel(const void* __restrict__ x, in
         }
     };
     fill(std::true_type{}, 0.0f, 0);
-    const int nval = live ? (E - c0 < 0 ? 0 : E - c0 < EPL ? E - c0 : EPL) : 0;
-    int npop = 0;
     float lv = 0.0f;
     int lu = 0;
-    const bool staged = k <= LPR;  // wave-uniform
-    float ov = 0.0f;
-    int oc = 0;
-    for (int j = 0; j < k; ++j) {
-        const float mrow = row_max_candidates<LPR>(tv[0]);
-        const unsigned long long hit = __ballot(tv[0] == mrow) & row_bits;
-        const int w = __ffsll((long long)hit) - 1;
-        const bool win = lane == w;
-        if (staged) {
-            const int col = __builtin_amdgcn_ds_bpermute(w << 2, c0 + tu[0]);
-            ov = sub == j ? mrow : ov;
-            oc = sub == j ? col : oc;
-        } else if (win && live) {
-            st_any<DT>(y, r * k + j, tv[0] / s);
-            eidx[r * k + j] = fin ? E : c0 + tu[0];
-            ridx[r * k + j] = (int32_t)((int64_t)j * rows + r);
-        }
+    // the row's winner (row lane wsub, the lowest holding the row maximum); the winner pops its
+    // head, and a lane whose list that empties refills it (a lane without values left rebuilds an
+    // empty list, which is harmless) unless it was the last round
+    auto winner = [&](const float mrow) {
+        const unsigned long long hit = __ballot(tv[0] == mrow);
+        if constexpr (LPR == 64) return __ffsll((long long)hit) - 1;
+        else return __ffs((unsigned)(hit >> (grp * LPR)) & ((1u << LPR) - 1u)) - 1;
+    };
+    auto pop = [&](const bool win, const int j) {
         if (win) {
             lv = tv[0];
             lu = tu[0];
@@ -851,17 +839,39 @@ __global__ __launch_bounds__(256) void mgt_kernel(const void* __restrict__ x, in
                 tu[t] = tu[t + 1];
             }
             tv[T - 1] = -1.0f;
-            ++npop;
         }
-        const bool refill = win && tv[0] < 0.0f && npop < nval && j + 1 < k;
-        if (__ballot(refill) != 0ull) {
+        const bool refill = win && tv[0] < 0.0f;
+        if (j + 1 < k && __ballot(refill) != 0ull) {
             if (refill) fill(std::false_type{}, lv, lu);
         }
-    }
-    if (staged && live && sub < k) {
-        st_any<DT>(y, r * k + sub, ov / s);
-        eidx[r * k + sub] = fin ? E : oc;
-        ridx[r * k + sub] = (int32_t)((int64_t)sub * rows + r);
+    };
+    if (k <= LPR) {
+        float ov = 0.0f;
+        int oc = 0;
+        for (int j = 0; j < k; ++j) {
+            const float mrow = row_max_candidates<LPR>(tv[0]);
+            const int wsub = winner(mrow);
+            const int col = __builtin_amdgcn_ds_bpermute((grp * LPR + wsub) << 2, c0 + tu[0]);
+            ov = sub == j ? mrow : ov;
+            oc = sub == j ? col : oc;
+            pop(sub == wsub, j);
+        }
+        if (live && sub < k) {
+            st_any<DT>(y, r * k + sub, ov / s);
+            eidx[r * k + sub] = fin ? E : oc;
+            ridx[r * k + sub] = (int32_t)((int64_t)sub * rows + r);
+        }
+    } else {
+        for (int j = 0; j < k; ++j) {
+            const float mrow = row_max_candidates<LPR>(tv[0]);
+            const bool win = sub == winner(mrow);
+            if (win && live) {
+                st_any<DT>(y, r * k + j, tv[0] / s);
+                eidx[r * k + j] = fin ? E : c0 + tu[0];
+                ridx[r * k + j] = (int32_t)((int64_t)j * rows + r);
+            }
+            pop(win, j);
+        }
     }
 }
 
