@@ -75,7 +75,53 @@ def main():
     bg = bf16_bits(rg.standard_normal((4, 48)).astype(np.float32))
     yg = orc.grouped_matmul(xg, wg, gl, bg, dtype="bf16", bias_dtype="bf16")
     np.savez_compressed(os.path.join(HERE, "grouped_matmul.npz"), x=xg, w=wg, bias=bg, group_list=gl, y=yg)
+    routing_fixtures()
     print("wrote fixtures to", HERE)
+
+
+def routing_fixtures():
+    """The routing operators around the experts, each on a small case with its edge conditions."""
+    rr = np.random.default_rng(2026)
+    # MoeGatingTopKSoftmax: fp32 [12, 64], top 4, an all-tied row and finished rows
+    x = rr.standard_normal((12, 64)).astype(np.float32)
+    x[3] = 0.25
+    fin = (rr.random(12) < 0.25).astype(np.uint8)
+    y, ei, ri = orc.moe_gating_top_k_softmax(x, "f32", 4, fin)
+    np.savez_compressed(os.path.join(HERE, "moe_gating.npz"), x=x, finished=fin, k=np.int64(4), y=y,
+                        expert_idx=ei, row_idx=ri)
+    # MoeReRouting: bf16 tokens [A = 24, H = 40] over 3 ranks x 4 experts (empty cells), scales
+    cnt = rr.integers(0, 4, (3, 4)).astype(np.int32)
+    cnt[1, 2] = 0
+    A = int(cnt.sum()) + 3
+    tok = bf16_bits(rr.standard_normal((A, 40)).astype(np.float32))
+    sc = rr.uniform(0.5, 1.5, A).astype(np.float32)
+    pt, ps, pi, etn, total = orc.moe_re_routing(tok, cnt, sc)
+    np.savez_compressed(os.path.join(HERE, "moe_re_routing.npz"), tokens=tok, counts=cnt, scales=sc,
+                        total=np.int64(total), permute_tokens=pt, permute_scales=ps, permute_idx=pi,
+                        expert_token_num=etn)
+    # MoeFinalizeRouting: bf16, 6 rows x top 2, H 24, both skips, bias over 3 experts, fp32 scales,
+    # a dropped slot (-1); drop_pad_mode 0 (column-major expanded_src_to_dst_row)
+    R, K, H, E = 6, 2, 24, 3
+    epr = bf16_bits(rr.standard_normal((R * K, H)).astype(np.float32))
+    perm = rr.permutation(R * K).astype(np.int32).reshape(R, K)
+    perm[2, 1] = -1
+    esdr = np.ascontiguousarray(perm.T).reshape(-1)
+    s1 = bf16_bits(rr.standard_normal((R, H)).astype(np.float32))
+    s2 = bf16_bits(rr.standard_normal((R, H)).astype(np.float32))
+    bias = bf16_bits(rr.standard_normal((E, H)).astype(np.float32))
+    scl = rr.random((R, K)).astype(np.float32)
+    ex = rr.integers(0, E, (R, K)).astype(np.int32)
+    out = orc.moe_finalize_routing(epr, "bf16", esdr, K, s1, s2, bias, scl, "f32", ex, 0)
+    np.savez_compressed(os.path.join(HERE, "moe_finalize_routing.npz"), epr=epr, esdr=esdr, skip1=s1, skip2=s2,
+                        bias=bias, scales=scl, expert=ex, k=np.int64(K), out=out)
+    # DequantSwigluQuant: int32 x [5, 2 x 48] with weight, activation and quant scales
+    xq = rr.integers(-40000, 40000, (5, 96)).astype(np.int32)
+    wsq = rr.uniform(1e-5, 1e-4, 96).astype(np.float32)
+    asq = rr.uniform(0.01, 0.06, 5).astype(np.float32)
+    qsq = rr.uniform(0.5, 1.5, 48).astype(np.float32)
+    yq, sq = orc.dequant_swiglu_quant(xq, "i32", wsq, asq, qsq, False)
+    np.savez_compressed(os.path.join(HERE, "dequant_swiglu_quant.npz"), x=xq, weight_scale=wsq,
+                        activation_scale=asq, quant_scale=qsq, y=yq, scale=sq)
 
 
 if __name__ == "__main__":

@@ -285,3 +285,46 @@ def test_moe_re_routing_large_cell_table(cb, orc):
     np.testing.assert_array_equal(etn.cpu().numpy(), r_etn)
     np.testing.assert_array_equal(pi.cpu().numpy(), r_idx)
     np.testing.assert_array_equal(bits16(pt), r_out)
+
+
+# ---------------------------------------------------------------------------------------------
+# committed golden fixtures of the routing operators
+# ---------------------------------------------------------------------------------------------
+def _golden(name):
+    import os
+    return np.load(os.path.join(os.path.dirname(__file__), "golden", name + ".npz"), allow_pickle=False)
+
+
+def _bf16_dev(bits):
+    return torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).to(DEV)
+
+
+def test_golden_routing_fixtures(cb):
+    g = _golden("moe_gating")
+    y, ei, ri = cb.moe_gating_top_k_softmax(torch.from_numpy(g["x"]).to(DEV),
+                                            torch.from_numpy(g["finished"].astype(bool)).to(DEV), int(g["k"]))
+    np.testing.assert_array_equal(ei.cpu().numpy(), g["expert_idx"])
+    np.testing.assert_array_equal(ri.cpu().numpy(), g["row_idx"])
+    np.testing.assert_allclose(y.cpu().numpy(), g["y"], rtol=1e-5, atol=1e-9)
+
+    g = _golden("moe_re_routing")
+    total = int(g["total"])
+    pt, ps, pi, etn = cb.moe_re_routing(_bf16_dev(g["tokens"]), torch.from_numpy(g["counts"]).to(DEV),
+                                        torch.from_numpy(g["scales"]).to(DEV))
+    np.testing.assert_array_equal(bits16(pt)[:total], g["permute_tokens"][:total])
+    np.testing.assert_array_equal(ps.cpu().numpy()[:total], g["permute_scales"][:total])
+    np.testing.assert_array_equal(pi.cpu().numpy()[:total], g["permute_idx"][:total])
+    np.testing.assert_array_equal(etn.cpu().numpy(), g["expert_token_num"])
+
+    g = _golden("moe_finalize_routing")
+    out = cb.moe_finalize_routing(_bf16_dev(g["epr"]), torch.from_numpy(g["esdr"]).to(DEV), _bf16_dev(g["skip1"]),
+                                  _bf16_dev(g["skip2"]), _bf16_dev(g["bias"]), torch.from_numpy(g["scales"]).to(DEV),
+                                  torch.from_numpy(g["expert"]).to(DEV), 0)
+    np.testing.assert_array_equal(bits16(out), g["out"])
+
+    g = _golden("dequant_swiglu_quant")
+    y, s = cb.dequant_swiglu_quant(torch.from_numpy(g["x"]).to(DEV), torch.from_numpy(g["weight_scale"]).to(DEV),
+                                   torch.from_numpy(g["activation_scale"]).to(DEV),
+                                   torch.from_numpy(g["quant_scale"]).to(DEV), False)
+    _assert_i8(y.cpu().numpy(), g["y"], "dequant_swiglu_quant fixture")
+    np.testing.assert_allclose(s.cpu().numpy(), g["scale"], rtol=1e-5)

@@ -240,3 +240,56 @@ def test_gating_ties_and_finished():
     np.testing.assert_array_equal(ei[1], [3, 9, 12, 0])
     np.testing.assert_array_equal(ei[2], [E] * k)  # finished row
     np.testing.assert_allclose(y[2], y[0])  # values unchanged by finished
+
+
+# ---------------------------------------------------------------------------------------------
+# golden fixtures of the routing operators (frozen oracle outputs, regenerated only by
+# tests/golden/make_golden.py); each also checked against a property the fixture must hold
+# ---------------------------------------------------------------------------------------------
+def _golden(name):
+    import os
+    p = os.path.join(os.path.dirname(__file__), "golden", name + ".npz")
+    if not os.path.exists(p):
+        pytest.skip(f"missing fixture {p}")
+    return np.load(p, allow_pickle=False)
+
+
+def test_golden_moe_gating():
+    g = _golden("moe_gating")
+    k = int(g["k"])
+    y, ei, ri = orc.moe_gating_top_k_softmax(g["x"], "f32", k, g["finished"])
+    np.testing.assert_array_equal(y, g["y"])
+    np.testing.assert_array_equal(ei, g["expert_idx"])
+    np.testing.assert_array_equal(ri, g["row_idx"])
+    # finished rows name expert E; the all-tied row picks columns 0..k-1
+    E = g["x"].shape[1]
+    assert (g["expert_idx"][g["finished"] == 1] == E).all()
+    if not g["finished"][3]:
+        np.testing.assert_array_equal(g["expert_idx"][3], np.arange(k))
+
+
+def test_golden_moe_re_routing():
+    g = _golden("moe_re_routing")
+    pt, ps, pi, etn, total = orc.moe_re_routing(g["tokens"], g["counts"], g["scales"])
+    assert total == int(g["total"])
+    for name, got in (("permute_tokens", pt), ("permute_scales", ps), ("permute_idx", pi),
+                      ("expert_token_num", etn)):
+        np.testing.assert_array_equal(got, g[name], err_msg=name)
+    # rows move unchanged: permute_tokens[i] = tokens[permute_idx[i]]
+    np.testing.assert_array_equal(g["permute_tokens"][:total], g["tokens"][g["permute_idx"][:total]])
+    np.testing.assert_array_equal(g["expert_token_num"], g["counts"].sum(0))
+
+
+def test_golden_moe_finalize_routing():
+    g = _golden("moe_finalize_routing")
+    out = orc.moe_finalize_routing(g["epr"], "bf16", g["esdr"], int(g["k"]), g["skip1"], g["skip2"], g["bias"],
+                                   g["scales"], "f32", g["expert"], 0)
+    np.testing.assert_array_equal(out, g["out"])
+
+
+def test_golden_dequant_swiglu_quant():
+    g = _golden("dequant_swiglu_quant")
+    y, s = orc.dequant_swiglu_quant(g["x"], "i32", g["weight_scale"], g["activation_scale"], g["quant_scale"], False)
+    np.testing.assert_array_equal(y, g["y"])
+    np.testing.assert_array_equal(s, g["scale"])
+    assert (np.abs(g["y"].astype(np.int32)).max(axis=1) == 127).all()  # each row reaches full scale
