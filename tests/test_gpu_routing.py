@@ -177,7 +177,7 @@ def test_dequant_swiglu_quant_zero_rows_and_checks(cb):
 # ---------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("rows,E,k", [(4096, 256, 8), (2000, 256, 1), (1000, 64, 6), (77, 8, 2), (500, 256, 2), (33, 2048, 16),
-                                      (9, 130, 130), (5, 1, 1), (16, 16, 16)])
+                                      (9, 130, 130), (20, 300, 100), (5, 1, 1), (16, 16, 16)])
 @pytest.mark.parametrize("fin", [False, True])
 def test_moe_gating_top_k_softmax(cb, orc, dt, rows, E, k, fin):
     g = gen(rows + E * 3 + k)
