@@ -197,3 +197,24 @@ def test_gmsq_status_query_host_paths(lib):
     assert so.cb_grouped_matmul_swiglu_quant_status(ctypes.addressof(buf), 16, 64, 2, None, None) == L.CB_ERR_NULL_POINTER
     assert so.cb_grouped_matmul_swiglu_quant_status(ctypes.addressof(buf), 0, 64, 2, ctypes.byref(st), None) == L.CB_OK
     assert st.value == 0
+
+
+def test_abi_from_c(lib, tmp_path):
+    """The header compiles as C99 under -Wall -Wextra -pedantic -Werror, and a C program linked
+    against the library gets each validation status back (tests/abi_c/abi_from_c.c)."""
+    import shutil
+    import subprocess
+    L, _ = lib
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    so = L.LIB_PATH
+    src = os.path.join(ROOT, "tests", "abi_c", "abi_from_c.c")
+    exe = str(tmp_path / "abi_from_c")
+    libdir, libfile = os.path.split(os.path.abspath(so))
+    cmd = [cc, "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror", "-I", os.path.join(ROOT, "include"), src,
+           os.path.join(libdir, libfile), "-Wl,-rpath," + libdir, "-o", exe]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout + r.stderr
